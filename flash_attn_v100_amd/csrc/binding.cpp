@@ -1,0 +1,519 @@
+// PyTorch-ROCm extension exposing the reference module's Python API
+// (module `flash_attn_v100`, flash_attn.cpp:224-255) on top of the C ABI in
+// include/flash_attn_mi355x.h.
+//
+// Each function keeps the reference's positional signature, its argument
+// validation (same conditions, same messages, raised as RuntimeError through
+// TORCH_CHECK) and its output contract, then calls one fa_* entry point on the
+// caller's current HIP stream (the `_stream` variants: on the given stream).
+// Names the MI355X build does not implement raise RuntimeError.
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPCachingAllocatorMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <cmath>
+#include <vector>
+
+#include "../../include/flash_attn_mi355x.h"
+
+namespace {
+
+using c10::hip::HIPGuardMasqueradingAsCUDA;
+using c10::hip::HIPStreamGuardMasqueradingAsCUDA;
+
+// Validation macros and helpers with the reference's conditions and messages
+// (flash_attn_kernel.cu:15-30, :122-249).
+#define CHECK_CUDA(x) TORCH_CHECK(x.device().is_cuda(), #x " must be a CUDA tensor")
+#define CHECK_CONTIGUOUS(x) TORCH_CHECK(x.is_contiguous(), #x " must be a contiguous tensor")
+#define CHECK_INPUT(x) \
+  CHECK_CUDA(x);       \
+  CHECK_CONTIGUOUS(x)
+#define CHECK_DIM(x, expected_dim) TORCH_CHECK(x.dim() == expected_dim, #x " must be a " #expected_dim "D tensor")
+#define CHECK_SAME_DEVICE(x, y) TORCH_CHECK(x.device() == y.device(), #x " and " #y " must be on the same device")
+#define CHECK_SAME_DTYPE(x, y) TORCH_CHECK(x.dtype() == y.dtype(), #x " and " #y " must have the same dtype")
+
+constexpr int64_t kMaxD = 128;       // MAX_D (flash_attn_kernel.cu:35)
+constexpr int64_t kMaxDLarge = 256;  // MAX_D_LARGE (flash_attn_kernel.cu:36)
+constexpr int64_t kPage = 16;        // PAGE_BLOCK_SIZE (flash_attn_kernel.cu:3389)
+
+void check_fa(int rc) {
+  TORCH_CHECK(rc == FA_OK, "flash_attn_v100 (MI355X): ", fa_last_error());
+}
+
+void* cur_stream() { return static_cast<void*>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream()); }
+
+int to_int(int64_t x, const char* what) {
+  TORCH_CHECK(x >= 0 && x <= INT32_MAX, what, " out of int32 range");
+  return static_cast<int>(x);
+}
+
+void check_mha_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  CHECK_DIM(q, 4);
+  CHECK_DIM(k, 4);
+  CHECK_DIM(v, 4);
+  CHECK_SAME_DEVICE(q, k);
+  CHECK_SAME_DEVICE(q, v);
+  CHECK_SAME_DTYPE(q, k);
+  CHECK_SAME_DTYPE(q, v);
+  TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape");
+  TORCH_CHECK(q.sizes() == v.sizes(), "q and v must have the same shape");
+}
+
+void check_decode_mha_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  CHECK_DIM(q, 4);
+  CHECK_DIM(k, 4);
+  CHECK_DIM(v, 4);
+  CHECK_SAME_DEVICE(q, k);
+  CHECK_SAME_DEVICE(q, v);
+  CHECK_SAME_DTYPE(q, k);
+  CHECK_SAME_DTYPE(q, v);
+  TORCH_CHECK(q.size(0) == k.size(0) && q.size(0) == v.size(0), "q, k, v batch size must match");
+  TORCH_CHECK(q.size(1) == k.size(1) && q.size(1) == v.size(1), "q, k, v head count must match");
+  TORCH_CHECK(q.size(3) == k.size(3) && q.size(3) == v.size(3), "q, k, v head dimension must match");
+  TORCH_CHECK(k.size(2) == v.size(2), "k and v sequence length must match");
+}
+
+void check_prefill_gqa_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  CHECK_DIM(q, 4);
+  CHECK_DIM(k, 4);
+  CHECK_DIM(v, 4);
+  CHECK_SAME_DEVICE(q, k);
+  CHECK_SAME_DEVICE(q, v);
+  CHECK_SAME_DTYPE(q, k);
+  CHECK_SAME_DTYPE(q, v);
+  TORCH_CHECK(q.size(0) == k.size(0) && q.size(0) == v.size(0), "q, k, v batch size must match");
+  TORCH_CHECK(k.size(1) == v.size(1), "k and v must have the same number of heads");
+  TORCH_CHECK(q.size(2) == k.size(2) && q.size(2) == v.size(2), "q, k, v sequence length must match");
+  TORCH_CHECK(q.size(3) == k.size(3) && q.size(3) == v.size(3), "q, k, v head dimension must match");
+}
+
+void check_decode_gqa_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
+  CHECK_DIM(q, 4);
+  CHECK_DIM(k, 4);
+  CHECK_DIM(v, 4);
+  CHECK_SAME_DEVICE(q, k);
+  CHECK_SAME_DEVICE(q, v);
+  CHECK_SAME_DTYPE(q, k);
+  CHECK_SAME_DTYPE(q, v);
+  TORCH_CHECK(q.size(0) == k.size(0) && q.size(0) == v.size(0), "q, k, v batch size must match");
+  TORCH_CHECK(k.size(1) == v.size(1), "k and v must have the same number of heads");
+  TORCH_CHECK(k.size(2) == v.size(2), "k and v sequence length must match");
+  TORCH_CHECK(q.size(3) == k.size(3) && q.size(3) == v.size(3), "q, k, v head dimension must match");
+}
+
+void check_varlen_prefill_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                       const at::Tensor& cu_seqlens) {
+  CHECK_DIM(q, 3);
+  CHECK_DIM(k, 3);
+  CHECK_DIM(v, 3);
+  CHECK_DIM(cu_seqlens, 1);
+  CHECK_SAME_DEVICE(q, k);
+  CHECK_SAME_DEVICE(q, v);
+  CHECK_SAME_DEVICE(q, cu_seqlens);
+  CHECK_SAME_DTYPE(q, k);
+  CHECK_SAME_DTYPE(q, v);
+  TORCH_CHECK(k.size(0) == q.size(0) && v.size(0) == q.size(0), "k and v total length must match q");
+  TORCH_CHECK(k.size(1) == q.size(1) && v.size(1) == q.size(1), "k and v head count must match q");
+  TORCH_CHECK(k.size(2) == q.size(2) && v.size(2) == q.size(2), "k and v head dimension must match q");
+}
+
+void check_cache_len(int cache_len, int64_t seq_len) {
+  TORCH_CHECK(cache_len >= 0, "cache_len must be non-negative");
+  TORCH_CHECK(cache_len < seq_len, "cache_len must be less than sequence length");
+}
+
+void check_decode_gqa_output_tensor(const at::Tensor& out, const at::Tensor& q) {
+  CHECK_INPUT(out);
+  CHECK_DIM(out, 4);
+  CHECK_SAME_DEVICE(out, q);
+  CHECK_SAME_DTYPE(out, q);
+  TORCH_CHECK(out.size(0) == q.size(0), "out batch size must match q");
+  TORCH_CHECK(out.size(1) == q.size(1), "out head count must match q");
+  TORCH_CHECK(out.size(2) == 1, "out sequence length must be 1 for decode mode");
+  TORCH_CHECK(out.size(3) == q.size(3), "out head dimension must match q");
+}
+
+void check_prefill_gqa_output_tensor(const at::Tensor& out, const at::Tensor& q) {
+  CHECK_INPUT(out);
+  CHECK_DIM(out, 4);
+  CHECK_SAME_DEVICE(out, q);
+  CHECK_SAME_DTYPE(out, q);
+  TORCH_CHECK(out.sizes() == q.sizes(), "out shape must match q shape for prefill mode");
+}
+
+// Split-KV partials live in a torch-allocated scratch tensor on the launch stream.
+at::Tensor decode_workspace(const at::Tensor& q, int B, int H_Q, int H_KV, int max_len, int D) {
+  const size_t bytes = fa_decode_workspace_size(B, H_Q, H_KV, max_len, D);
+  return at::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, q.options().dtype(at::kByte));
+}
+
+// ---------------------------------------------------------------------------
+// Prefill
+
+void launch_prefill(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, at::Tensor& out, bool causal) {
+  check_fa(fa_prefill_fp16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), to_int(q.size(0), "B"),
+                           to_int(q.size(1), "H_Q"), to_int(k.size(1), "H_KV"), to_int(q.size(2), "N"),
+                           to_int(q.size(3), "D"), causal ? 1 : 0, cur_stream()));
+}
+
+// forward_prefill_gqa_fp16 (flash_attn_kernel.cu:2740-2768)
+at::Tensor forward_prefill_gqa_fp16(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_prefill_gqa_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  const auto H_Q = q.size(1), N = q.size(2), D = q.size(3), H_KV = k.size(1);
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(D <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  TORCH_CHECK(k.size(2) == N, "k sequence length must match q");
+  TORCH_CHECK(v.size(2) == N, "v sequence length must match q");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  launch_prefill(q, k, v, out, causal);
+  return out;
+}
+
+// forward_prefill_gqa_fp16_out (flash_attn_kernel.cu:2770-2794)
+at::Tensor forward_prefill_gqa_fp16_out(at::Tensor out, at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_prefill_gqa_input_shapes(q, k, v);
+  check_prefill_gqa_output_tensor(out, q);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(1) >= k.size(1), "H_Q must be >= H_KV");
+  TORCH_CHECK(q.size(1) % k.size(1) == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(q.size(3) <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  launch_prefill(q, k, v, out, causal);
+  return out;
+}
+
+// forward_fp16 (flash_attn_kernel.cu:1915-1962)
+at::Tensor forward_fp16(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_mha_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(3) <= kMaxDLarge, "D must be less than or equal to MAX_D_LARGE(256)");
+  if (q.size(3) > kMaxD) return forward_prefill_gqa_fp16(q, k, v, causal);
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  launch_prefill(q, k, v, out, causal);
+  return out;
+}
+
+// forward_fp16_warp (flash_attn_kernel.cu:1440-1484): same math as forward_fp16.
+at::Tensor forward_fp16_warp(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_mha_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(3) <= kMaxD, "D must be less than or equal to MAX_D(128)");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  launch_prefill(q, k, v, out, causal);
+  return out;
+}
+
+// forward_fp16_wmma (flash_attn_kernel.cu:2425-2468): the reference's tensor-core
+// variant; on gfx950 the one MFMA prefill kernel serves both names.
+at::Tensor forward_fp16_wmma(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_mha_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(3) % 16 == 0, "D must be multiple of 16 for WMMA");
+  TORCH_CHECK(q.size(3) <= kMaxD, "D must be less than or equal to MAX_D(128)");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  launch_prefill(q, k, v, out, causal);
+  return out;
+}
+
+// forward_prefill_gqa_fp16_warp (flash_attn_kernel.cu:3586-3637)
+at::Tensor forward_prefill_gqa_fp16_warp(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  return forward_prefill_gqa_fp16(q, k, v, causal);
+}
+
+// ---------------------------------------------------------------------------
+// Decode
+
+void launch_decode(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, at::Tensor& out, bool causal,
+                   int cache_len) {
+  const int B = to_int(q.size(0), "B"), H_Q = to_int(q.size(1), "H_Q"), H_KV = to_int(k.size(1), "H_KV");
+  const int N = to_int(k.size(2), "N"), D = to_int(q.size(3), "D");
+  auto ws = decode_workspace(q, B, H_Q, H_KV, N, D);
+  check_fa(fa_decode_fp16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H_Q, H_KV, N, D,
+                          causal ? 1 : 0, cache_len, ws.data_ptr(), static_cast<size_t>(ws.numel()),
+                          cur_stream()));
+}
+
+// forward_decode_gqa_fp16 (flash_attn_kernel.cu:1800-1833)
+at::Tensor forward_decode_gqa_fp16(at::Tensor q, at::Tensor k, at::Tensor v, bool causal, int cache_len) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_decode_gqa_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  const auto H_Q = q.size(1), H_KV = k.size(1);
+  TORCH_CHECK(H_KV == v.size(1), "k and v must have same number of heads");
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(q.size(3) <= kMaxDLarge, "D must be less than or equal to MAX_D_LARGE(256)");
+  check_cache_len(cache_len, k.size(2));
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty({q.size(0), H_Q, 1, q.size(3)}, q.options());
+  launch_decode(q, k, v, out, causal, cache_len);
+  return out;
+}
+
+// forward_decode_gqa_fp16_out (flash_attn_kernel.cu:1835-1861)
+at::Tensor forward_decode_gqa_fp16_out(at::Tensor out, at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
+                                       int cache_len) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_decode_gqa_input_shapes(q, k, v);
+  check_decode_gqa_output_tensor(out, q);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  TORCH_CHECK(q.size(1) >= k.size(1), "H_Q must be >= H_KV");
+  TORCH_CHECK(q.size(1) % k.size(1) == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(q.size(3) <= kMaxDLarge, "D must be less than or equal to MAX_D_LARGE(256)");
+  check_cache_len(cache_len, k.size(2));
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  launch_decode(q, k, v, out, causal, cache_len);
+  return out;
+}
+
+// forward_decode_gqa_fp16_stream (flash_attn_kernel.cu:3639-3673)
+at::Tensor forward_decode_gqa_fp16_stream(at::Tensor q, at::Tensor k, at::Tensor v, bool causal, int cache_len,
+                                          int64_t stream_int) {
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto ext = c10::hip::getStreamFromExternalMasqueradingAsCUDA(reinterpret_cast<hipStream_t>(stream_int),
+                                                               q.device().index());
+  HIPStreamGuardMasqueradingAsCUDA sguard(ext);
+  return forward_decode_gqa_fp16(q, k, v, causal, cache_len);
+}
+
+// forward_decode_fp16 (flash_attn_kernel.cu:1863-1913)
+at::Tensor forward_decode_fp16(at::Tensor q, at::Tensor k, at::Tensor v, bool causal, int cache_len) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_decode_mha_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  TORCH_CHECK(q.size(3) <= kMaxDLarge, "D must be less than or equal to MAX_D_LARGE(256)");
+  check_cache_len(cache_len, k.size(2));
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty({q.size(0), q.size(1), 1, q.size(3)}, q.options());
+  launch_decode(q, k, v, out, causal, cache_len);
+  return out;
+}
+
+// forward_continuous_batching_fp16 (continuous_batching_kernel.cu:338-406)
+at::Tensor forward_continuous_batching_fp16(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor cache_lens,
+                                            bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  CHECK_INPUT(cache_lens);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q must be float16");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  TORCH_CHECK(cache_lens.dim() == 1, "cache_lens must be 1D tensor");
+  TORCH_CHECK(cache_lens.size(0) == q.size(0), "cache_lens size must match batch size");
+  const auto H_Q = q.size(1), H_KV = k.size(1), D = q.size(3);
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(D <= kMaxDLarge, "D must be <= MAX_D_CB_LARGE(256)");
+  // The reference reads these without checking (continuous_batching_kernel.cu:373-403);
+  // a mismatch there reads out of bounds, here it is an error.
+  TORCH_CHECK(cache_lens.dtype() == at::kInt, "cache_lens must be int32");
+  check_decode_gqa_input_shapes(q, k, v);
+  CHECK_SAME_DEVICE(q, cache_lens);
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int B = to_int(q.size(0), "B"), hq = to_int(H_Q, "H_Q"), hkv = to_int(H_KV, "H_KV");
+  const int max_N = to_int(k.size(2), "max_N"), d = to_int(D, "D");
+  auto out = at::empty({q.size(0), H_Q, 1, D}, q.options());
+  auto ws = decode_workspace(q, B, hq, hkv, max_N, d);
+  check_fa(fa_continuous_batching_fp16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                       cache_lens.data_ptr<int32_t>(), B, hq, hkv, max_N, d, causal ? 1 : 0,
+                                       ws.data_ptr(), static_cast<size_t>(ws.numel()), cur_stream()));
+  return out;
+}
+
+// forward_paged_decode_gqa_fp16 (flash_attn_kernel.cu:3516-3584)
+at::Tensor forward_paged_decode_gqa_fp16(at::Tensor q, at::Tensor k_cache, at::Tensor v_cache,
+                                         at::Tensor block_table, at::Tensor seq_lens, int max_num_blocks) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k_cache);
+  CHECK_INPUT(v_cache);
+  CHECK_INPUT(block_table);
+  CHECK_INPUT(seq_lens);
+  CHECK_DIM(q, 4);
+  CHECK_DIM(k_cache, 4);
+  CHECK_DIM(v_cache, 4);
+  CHECK_DIM(block_table, 2);
+  CHECK_DIM(seq_lens, 1);
+  CHECK_SAME_DEVICE(q, k_cache);
+  CHECK_SAME_DEVICE(q, v_cache);
+  CHECK_SAME_DEVICE(q, block_table);
+  CHECK_SAME_DEVICE(q, seq_lens);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q must be float16");
+  TORCH_CHECK(k_cache.dtype() == at::kHalf, "k_cache must be float16");
+  TORCH_CHECK(v_cache.dtype() == at::kHalf, "v_cache must be float16");
+  TORCH_CHECK(block_table.dtype() == at::kInt, "block_table must be int32");
+  TORCH_CHECK(seq_lens.dtype() == at::kInt, "seq_lens must be int32");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  const auto B = q.size(0), H_Q = q.size(1), H_KV = k_cache.size(1), D = q.size(3);
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(D <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  TORCH_CHECK(k_cache.size(2) == kPage, "k_cache block size mismatch");
+  TORCH_CHECK(v_cache.size(2) == kPage, "v_cache block size mismatch");
+  TORCH_CHECK(block_table.size(0) == B, "block_table batch size must match q");
+  TORCH_CHECK(seq_lens.size(0) == B, "seq_lens batch size must match q");
+  // Unchecked in the reference, which then addresses the caches with q's D.
+  TORCH_CHECK(k_cache.sizes() == v_cache.sizes(), "k_cache and v_cache must have the same shape");
+  TORCH_CHECK(k_cache.size(3) == D, "k_cache head dimension must match q");
+  TORCH_CHECK(max_num_blocks >= 0, "max_num_blocks must be non-negative");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int b = to_int(B, "B"), hq = to_int(H_Q, "H_Q"), hkv = to_int(H_KV, "H_KV"), d = to_int(D, "D");
+  auto out = at::empty({B, H_Q, 1, D}, q.options());
+  auto ws = decode_workspace(q, b, hq, hkv, max_num_blocks * static_cast<int>(kPage), d);
+  check_fa(fa_paged_decode_gqa_fp16(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
+                                    block_table.data_ptr<int32_t>(), block_table.numel(),
+                                    seq_lens.data_ptr<int32_t>(), b, hq, hkv, d,
+                                    to_int(k_cache.size(0), "num_pages"), max_num_blocks, ws.data_ptr(),
+                                    static_cast<size_t>(ws.numel()), cur_stream()));
+  return out;
+}
+
+// forward_decode_int8_gqa (flash_attn_kernel.cu:2941-3003)
+at::Tensor forward_decode_int8_gqa(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor q_scale,
+                                   at::Tensor k_scale, int cache_len) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  CHECK_INPUT(q_scale);
+  CHECK_INPUT(k_scale);
+  check_decode_gqa_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(q_scale.dtype() == at::kFloat, "q_scale must be float32");
+  TORCH_CHECK(k_scale.dtype() == at::kFloat, "k_scale must be float32");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  const auto B = q.size(0), H_Q = q.size(1), H_KV = k.size(1), N = k.size(2), D = q.size(3);
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(D <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  TORCH_CHECK(q_scale.dim() >= 2 && q_scale.size(0) == B && q_scale.size(1) == H_Q, "q_scale must be [B, H_Q]");
+  TORCH_CHECK(k_scale.dim() >= 3 && k_scale.size(0) == B && k_scale.size(1) == H_KV && k_scale.size(2) == N,
+              "k_scale must be [B, H_KV, N]");
+  CHECK_SAME_DEVICE(q, q_scale);
+  CHECK_SAME_DEVICE(q, k_scale);
+  check_cache_len(cache_len, N);
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  const int b = to_int(B, "B"), hq = to_int(H_Q, "H_Q"), hkv = to_int(H_KV, "H_KV");
+  const int n = to_int(N, "N"), d = to_int(D, "D");
+  auto out = at::empty({B, H_Q, 1, D}, q.options());
+  auto ws = decode_workspace(q, b, hq, hkv, n, d);
+  check_fa(fa_decode_int8_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                              q_scale.data_ptr<float>(), k_scale.data_ptr<float>(), b, hq, hkv, n, d, cache_len,
+                              ws.data_ptr(), static_cast<size_t>(ws.numel()), cur_stream()));
+  return out;
+}
+
+// ---------------------------------------------------------------------------
+// Varlen prefill
+
+// forward_varlen_prefill_fp16 (flash_attn_kernel.cu:3354-3387)
+at::Tensor forward_varlen_prefill_fp16(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor cu_seqlens,
+                                       int max_seqlen, bool causal) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  CHECK_INPUT(cu_seqlens);
+  check_varlen_prefill_input_shapes(q, k, v, cu_seqlens);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q, k, v must be float16");
+  TORCH_CHECK(cu_seqlens.dtype() == at::kInt, "cu_seqlens must be int32");
+  const auto total_q = q.size(0), H = q.size(1), D = q.size(2);
+  const auto batch_size = cu_seqlens.size(0) - 1;
+  TORCH_CHECK(D <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  TORCH_CHECK(k.size(0) == total_q, "k and q must have same total length");
+  TORCH_CHECK(v.size(0) == total_q, "v and q must have same total length");
+  TORCH_CHECK(max_seqlen > 0, "max_seqlen must be positive");
+  TORCH_CHECK(batch_size > 0, "cu_seqlens must contain at least one sequence");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::zeros_like(q);
+  // Rows a sequence's reference grid reaches: tile*ceil(max_seqlen/tile), tile 32
+  // for D <= 128 and 8 above (flash_attn_kernel.cu:3319-3320, :3336-3337).
+  const int64_t tile = D <= kMaxD ? 32 : 8;
+  const int64_t row_limit = ((static_cast<int64_t>(max_seqlen) + tile - 1) / tile) * tile;
+  check_fa(fa_varlen_prefill_fp16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                  cu_seqlens.data_ptr<int32_t>(), to_int(batch_size, "batch"),
+                                  to_int(total_q, "total"), to_int(H, "H"), to_int(D, "D"), max_seqlen,
+                                  to_int(std::min<int64_t>(row_limit, INT32_MAX), "row_limit"), causal ? 1 : 0,
+                                  cur_stream()));
+  return out;
+}
+
+// forward_varlen_prefill_fp16_stream (flash_attn_kernel.cu:3675-3712)
+at::Tensor forward_varlen_prefill_fp16_stream(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor cu_seqlens,
+                                              int max_seqlen, bool causal, int64_t stream_int) {
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto ext = c10::hip::getStreamFromExternalMasqueradingAsCUDA(reinterpret_cast<hipStream_t>(stream_int),
+                                                               q.device().index());
+  HIPStreamGuardMasqueradingAsCUDA sguard(ext);
+  return forward_varlen_prefill_fp16(q, k, v, cu_seqlens, max_seqlen, causal);
+}
+
+// ---------------------------------------------------------------------------
+// Names of the reference module that are outside the MI355X hot path.
+
+void not_implemented(const char* name) {
+  TORCH_CHECK(false, "flash_attn_v100.", name,
+              " is not implemented in the MI355X build (hot path: forward_fp16, forward_fp16_wmma, "
+              "forward_decode_fp16, forward_decode_gqa_fp16, forward_continuous_batching_fp16, "
+              "forward_varlen_prefill_fp16, forward_paged_decode_gqa_fp16, forward_decode_int8_gqa)");
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("forward_fp16", &forward_fp16, "Flash attention forward, fp16 (MI355X MFMA)");
+  m.def("forward_fp16_warp", &forward_fp16_warp, "Flash attention forward, fp16 (MI355X MFMA)");
+  m.def("forward_fp16_wmma", &forward_fp16_wmma, "Flash attention forward, fp16 (MI355X MFMA)");
+  m.def("forward_prefill_gqa_fp16", &forward_prefill_gqa_fp16, "GQA/MQA prefill, fp16 (MI355X MFMA)");
+  m.def("forward_prefill_gqa_fp16_out", &forward_prefill_gqa_fp16_out, "GQA/MQA prefill into out (MI355X)");
+  m.def("forward_prefill_gqa_fp16_warp", &forward_prefill_gqa_fp16_warp, "GQA/MQA prefill, fp16 (MI355X MFMA)");
+  m.def("forward_decode_fp16", &forward_decode_fp16, "MHA decode with KV cache (MI355X split-KV)");
+  m.def("forward_decode_gqa_fp16", &forward_decode_gqa_fp16, "GQA/MQA decode with KV cache (MI355X split-KV)");
+  m.def("forward_decode_gqa_fp16_out", &forward_decode_gqa_fp16_out, "GQA/MQA decode into out (MI355X)");
+  m.def("forward_decode_gqa_fp16_stream", &forward_decode_gqa_fp16_stream, "GQA decode on a given stream");
+  m.def("forward_continuous_batching_fp16", &forward_continuous_batching_fp16,
+        "Continuous-batching GQA decode (MI355X split-KV)");
+  m.def("forward_paged_decode_gqa_fp16", &forward_paged_decode_gqa_fp16, "Paged GQA decode (MI355X split-KV)");
+  m.def("forward_decode_int8_gqa", &forward_decode_int8_gqa, "INT8 GQA decode (MI355X sdot4)");
+  m.def("forward_varlen_prefill_fp16", &forward_varlen_prefill_fp16, "Packed varlen prefill (MI355X MFMA)");
+  m.def("forward_varlen_prefill_fp16_stream", &forward_varlen_prefill_fp16_stream,
+        "Packed varlen prefill on a given stream");
+  for (const char* name : {"forward", "forward_with_lse", "forward_fp16_with_lse", "backward", "async_h2d_transfer",
+                           "alloc_pinned_tensor", "pipeline_decode_step", "pipeline_decode_step_out",
+                           "speculative_verify", "forward_decode_int8_kv_cache_gqa", "token_eviction",
+                           "forward_decode_sliding_window_gqa", "cross_gpu_allreduce_fp16", "scatter_heads",
+                           "gather_heads"}) {
+    std::string n(name);
+    m.def(name, [n](pybind11::args, pybind11::kwargs) { not_implemented(n.c_str()); }, "Not implemented on MI355X");
+  }
+  m.def("_fa_version", []() { return std::string(fa_version()); });
+}

@@ -1,0 +1,92 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Wavefronts are 64 lanes.  Cross-lane reductions inside a 16-lane DPP row use
+// quad_perm / row_half_mirror / row_mirror moves (no LDS traffic); wider
+// reductions fall back to ds_swizzle/bpermute through __shfl_xor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+// Finite "no score yet" sentinel for running maxima in the log2 domain.  Every
+// real score of fp16 inputs is far above it, and exp2(sentinel - real) == 0.
+constexpr float kNegBig = -1.0e30f;
+
+// DPP control words (GFX9 encoding).
+constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+      0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+
+// Sum over aligned groups of W lanes (W in {8, 16, 32, 64}); every lane of the
+// group receives the group total.
+template <int W>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  x += dpp_mov<kDppQuadXor1>(x);
+  x += dpp_mov<kDppQuadXor2>(x);
+  x += dpp_mov<kDppRowHalfMirror>(x);
+  if constexpr (W >= 16) x += dpp_mov<kDppRowMirror>(x);
+  if constexpr (W >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (W >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+template <int W>
+__device__ __forceinline__ int group_sum_i(int x) {
+  static_assert(W == 8 || W == 16 || W == 32 || W == 64, "group width");
+  x += dpp_mov_i<kDppQuadXor1>(x);
+  x += dpp_mov_i<kDppQuadXor2>(x);
+  x += dpp_mov_i<kDppRowHalfMirror>(x);
+  if constexpr (W >= 16) x += dpp_mov_i<kDppRowMirror>(x);
+  if constexpr (W >= 32) x += __shfl_xor(x, 16, 64);
+  if constexpr (W >= 64) x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// Eight fp16 values starting at column `col` of a row of length `d`.  VEC: the
+// row base is 16-byte aligned and d % 8 == 0, so one dwordx4 load serves.
+template <bool VEC>
+__device__ __forceinline__ u32x4 load_row8(const half_t* row, int col, int d) {
+  if constexpr (VEC) {
+    if (col < d) return *reinterpret_cast<const u32x4*>(row + col);
+    return u32x4{0u, 0u, 0u, 0u};
+  } else {
+    half8_t h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (col + j < d) ? row[col + j] : (half_t)0.0f;
+    return __builtin_bit_cast(u32x4, h);
+  }
+}
+
+}  // namespace fa

@@ -1,0 +1,141 @@
+/*
+ * C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Plain pointers and sizes only: no torch, no HIP types in the signatures
+ * (`stream` is a hipStream_t passed as void*, NULL = the null stream).  Every
+ * tensor is a dense row-major fp16 array in device memory unless stated.  The
+ * library never allocates: split-KV decode entry points take a caller-owned
+ * device workspace whose size comes from fa_decode_workspace_size().  All calls
+ * are asynchronous on `stream`, stateless and reentrant.
+ *
+ * Return value: FA_OK (0) or an FA_ERR_* code; fa_last_error() gives a
+ * human-readable message for the calling thread's most recent failure.
+ *
+ * Each entry point replaces one kernel launch of the reference extension
+ * (acproject/flash_attn_v100); the reference interface it stands in for is cited
+ * as file:line under the reference tree.
+ */
+#ifndef FLASH_ATTN_MI355X_H
+#define FLASH_ATTN_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FA_OK = 0,
+  FA_ERR_INVALID_ARG = 1,   /* shape / pointer / size argument rejected     */
+  FA_ERR_WORKSPACE = 2,     /* workspace missing or smaller than required   */
+  FA_ERR_UNSUPPORTED = 3,   /* valid request outside what the kernels cover */
+  FA_ERR_HIP = 4            /* a HIP runtime call or kernel launch failed   */
+};
+
+/* Message describing the calling thread's last non-OK return. */
+const char* fa_last_error(void);
+
+/* Library version string ("<major>.<minor>.<patch> gfx950"). */
+const char* fa_version(void);
+
+/*
+ * Causal / full self-attention prefill, MFMA-tiled.
+ *   q [B, H_Q, N, D], k/v [B, H_KV, N, D], o [B, H_Q, N, D]; H_Q % H_KV == 0,
+ *   1 <= D <= 256.  Causal masks key j > query i.  Scale 1/sqrt(D).
+ * Replaces the launches behind forward_fp16 (flash_attn_kernel.cu:1915-1962),
+ * forward_fp16_wmma (:2425-2468) and forward_prefill_gqa_fp16 (:2740-2794,
+ * launch_prefill_gqa_fp16 :316-366).
+ */
+int fa_prefill_fp16(const void* q, const void* k, const void* v, void* o,
+                    int B, int H_Q, int H_KV, int N, int D, int causal,
+                    void* stream);
+
+/*
+ * Packed variable-length prefill.
+ *   q/k/v/o [total, H, D]; cu_seqlens int32 [batch + 1] in device memory.
+ *   Sequence b owns rows [cu[b], cu[b+1]); only its first `row_limit` rows are
+ *   written (the reference's grid covers tile*ceil(max_seqlen/tile) rows per
+ *   sequence, with tile 32 for D <= 128 and 8 above); other rows are untouched.
+ * Replaces launch_varlen_prefill_fp16_on_stream (flash_attn_kernel.cu:3302-3352)
+ * behind forward_varlen_prefill_fp16 (:3354-3387) and its _stream variant
+ * (:3675-3712).
+ */
+int fa_varlen_prefill_fp16(const void* q, const void* k, const void* v, void* o,
+                           const int32_t* cu_seqlens, int batch, int total,
+                           int H, int D, int max_seqlen, int row_limit,
+                           int causal, void* stream);
+
+/*
+ * Workspace bytes the split-KV decode entry points need for a call with these
+ * sizes.  max_len = N (contiguous decode / INT8), max_N (continuous batching)
+ * or 16 * max_num_blocks (paged).  May be 0.
+ */
+size_t fa_decode_workspace_size(int B, int H_Q, int H_KV, int max_len, int D);
+
+/*
+ * Single-token decode against a contiguous KV cache (MHA when H_Q == H_KV).
+ *   q/o [B, H_Q, 1, D], k/v [B, H_KV, N, D]; 0 <= cache_len < N.
+ *   causal: keys j > cache_len are masked; otherwise all N keys attend.
+ * Replaces the launches behind forward_decode_fp16 (flash_attn_kernel.cu:1863-1913),
+ * forward_decode_gqa_fp16 (:1800-1833, launch_decode_gqa_fp16_on_stream
+ * :251-303), its _out (:1835-1861) and _stream (:3639-3673) variants.
+ */
+int fa_decode_fp16(const void* q, const void* k, const void* v, void* o,
+                   int B, int H_Q, int H_KV, int N, int D, int causal,
+                   int cache_len, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/*
+ * Continuous-batching decode: per-sequence cache lengths.
+ *   q/o [B, H_Q, 1, D], k/v [B, H_KV, max_N, D], cache_lens int32 [B] (device).
+ *   Sequence b attends keys [0, min(cache_lens[b] + 1, max_N)); an empty range
+ *   yields NaN, as 0/0 does in the reference.
+ * Replaces the launch in flash_attn_forward_continuous_batching_fp16
+ * (continuous_batching_kernel.cu:338-406).
+ */
+int fa_continuous_batching_fp16(const void* q, const void* k, const void* v,
+                                void* o, const int32_t* cache_lens, int B,
+                                int H_Q, int H_KV, int max_N, int D, int causal,
+                                void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/*
+ * Paged GQA decode, 16-token pages.
+ *   q/o [B, H_Q, 1, D]; k_cache/v_cache [num_pages, H_KV, 16, D];
+ *   block_table int32 (device), read as flat[b * max_num_blocks + t / 16] for
+ *   token t (block_table_numel bounds that read); seq_lens int32 [B] (device).
+ *   Sequence b attends tokens [0, seq_lens[b]); seq_lens[b] <= 0, a page id
+ *   outside [0, num_pages) or a table index past block_table_numel yields NaN
+ *   for that sequence (the reference reads out of bounds there).
+ * Replaces the launch in flash_attn_forward_paged_decode_gqa_fp16
+ * (flash_attn_kernel.cu:3516-3584).
+ */
+int fa_paged_decode_gqa_fp16(const void* q, const void* k_cache,
+                             const void* v_cache, void* o,
+                             const int32_t* block_table,
+                             int64_t block_table_numel,
+                             const int32_t* seq_lens, int B, int H_Q, int H_KV,
+                             int D, int num_pages, int max_num_blocks,
+                             void* workspace, size_t workspace_bytes,
+                             void* stream);
+
+/*
+ * INT8 GQA decode: Q and K quantized to int8 (clamp(round(x / scale), +-127)),
+ * integer dot products, score = dot * q_s * k_s / sqrt(D); V stays fp16.
+ *   q/o [B, H_Q, 1, D], k/v [B, H_KV, N, D] fp16; q_scale float32 [B * H_Q];
+ *   k_scale float32, read as flat[b * H_KV + h_kv] (the reference kernel's own
+ *   indexing); keys j > cache_len always masked; 0 <= cache_len < N.
+ * Replaces the launch in flash_attn_forward_decode_int8_gqa
+ * (flash_attn_kernel.cu:2941-3003).
+ */
+int fa_decode_int8_gqa(const void* q, const void* k, const void* v, void* o,
+                       const float* q_scale, const float* k_scale, int B,
+                       int H_Q, int H_KV, int N, int D, int cache_len,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* FLASH_ATTN_MI355X_H */

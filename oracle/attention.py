@@ -1,0 +1,296 @@
+"""CPU restatement of the reference's attention semantics (TEST INFRASTRUCTURE ONLY).
+
+This module is the checker for the HIP kernels of ``flash_attn_v100_amd``. Only
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import it; the product path never calls it and has no CPU
+fallback.
+
+Every function restates one entry point of the reference extension
+(``flash_attn_v100``, sources under ``/root/reference``) as plain masked-softmax
+attention computed with PyTorch eager math on the CPU::
+
+    O = softmax(Q K^T / sqrt(D) + M) V      (fp16 inputs, fp32/fp64 arithmetic)
+
+The reference kernels are online-softmax loops (``m_i``/``l_i``/``acc``) whose
+result is mathematically this closed form; what differs between entry points is
+the mask ``M``, the index maps (GQA head mapping, paged address, packed varlen
+rows) and the INT8 quantization, which are restated exactly and cited line by
+line.  ``compute_dtype`` selects float32 (the CPU baseline; the reference test
+scripts' own precision) or float64 (error budgeting).
+
+Pinning: ``tests/test_oracle.py`` checks each function against an independent
+pure-Python fp64 loop restatement (``oracle/brute.py``) on tiny inputs, against
+closed forms (cache_len=0 -> V[0], identical keys -> mean(V), a dominant key ->
+its V row), against invariants (GQA == MHA on repeat-interleaved KV, paged ==
+contiguous on the gathered cache, varlen == per-segment prefill, continuous
+batching == per-row decode on the truncated cache) and against the committed
+fixtures in ``tests/golden/``.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+# Page size of the paged KV cache: ``PAGE_BLOCK_SIZE = 16`` (flash_attn_kernel.cu:3389).
+PAGE_BLOCK_SIZE = 16
+# Query-tile heights of the reference varlen kernels; they decide which packed
+# rows are ever written (flash_attn_kernel.cu:3336-3338 grid.x = ceil(max_seqlen/32)
+# for D<=128, :3319-3320 ceil(max_seqlen/8) for D>128).
+VARLEN_TILE_SMALL_D = 32
+VARLEN_TILE_LARGE_D = 8
+MAX_D_SMALL = 128  # MAX_D (flash_attn_kernel.cu:35)
+
+
+def host_scale_f32(d: int) -> torch.Tensor:
+    """``1.0f / std::sqrt((float)D)`` evaluated in float32 as the host wrappers do
+    (e.g. flash_attn_kernel.cu:1944, :2983)."""
+    return torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(d), dtype=torch.float32))
+
+
+def _softmax_rows(scores: torch.Tensor) -> torch.Tensor:
+    """Row softmax where a row with no unmasked key yields NaN.
+
+    The reference divides ``acc / l_i`` with ``l_i == 0`` and ``acc == 0`` for such
+    rows (e.g. flash_attn_kernel.cu:3511), i.e. 0/0 = NaN.  ``torch.softmax``
+    over an all ``-inf`` row gives the same NaN.
+    """
+    return torch.softmax(scores, dim=-1)
+
+
+def _attend(q, k, v, mask, compute_dtype):
+    """q [..., M, D], k/v [..., L, D], mask broadcastable to [..., M, L] (True = masked)."""
+    d = q.shape[-1]
+    qf = q.to(compute_dtype)
+    kf = k.to(compute_dtype)
+    vf = v.to(compute_dtype)
+    # Scale is 1/sqrt(D), computed on the host (flash_attn_kernel.cu:265, :1944).
+    scores = torch.matmul(qf, kf.transpose(-1, -2)) * (1.0 / math.sqrt(d))
+    if mask is not None:
+        scores = scores.masked_fill(mask, float("-inf"))
+    probs = _softmax_rows(scores)
+    if probs.shape[-1] == 0:
+        return torch.full(probs.shape[:-1] + (d,), float("nan"), dtype=compute_dtype)
+    return torch.matmul(probs, vf)
+
+
+def expand_kv(k: torch.Tensor, h_q: int) -> torch.Tensor:
+    """GQA head map ``h_kv = h_q / (H_Q / H_KV)`` (flash_attn_kernel.cu:1662, :2489;
+    continuous_batching_kernel.cu:62), i.e. ``repeat_interleave`` on the head dim."""
+    h_kv = k.shape[1]
+    return k.repeat_interleave(h_q // h_kv, dim=1)
+
+
+def prefill(q, k, v, causal: bool, compute_dtype=torch.float32):
+    """``forward_fp16`` / ``forward_fp16_wmma`` / ``forward_prefill_gqa_fp16``.
+
+    Q [B,H_Q,N,D], K/V [B,H_KV,N,D].  Causal masks key ``k_idx > q_idx`` (square,
+    top-left aligned): flash_attn_kernel.cu:1223 (a1), :2364 (a2 WMMA, mask applied
+    to the scaled score), :996 (D>128 path).  Non-causal attends all N keys.
+    """
+    n = q.shape[2]
+    k = expand_kv(k, q.shape[1])
+    v = expand_kv(v, q.shape[1])
+    mask = None
+    if causal:
+        mask = torch.triu(torch.ones(n, n, dtype=torch.bool), diagonal=1)
+    return _attend(q, k, v, mask, compute_dtype)
+
+
+def decode(q, k, v, causal: bool, cache_len: int, compute_dtype=torch.float32):
+    """``forward_decode_fp16`` (H_Q == H_KV) / ``forward_decode_gqa_fp16``.
+
+    Q [B,H_Q,1,D], K/V [B,H_KV,N,D].  Causal masks ``k_idx > cache_len``
+    (flash_attn_kernel.cu:1556, :1719, :846); non-causal attends all N rows.
+    """
+    n = k.shape[2]
+    k = expand_kv(k, q.shape[1])
+    v = expand_kv(v, q.shape[1])
+    mask = None
+    if causal:
+        mask = (torch.arange(n) > cache_len).view(1, 1, 1, n)
+    return _attend(q, k, v, mask, compute_dtype)
+
+
+def continuous_batching(q, k, v, cache_lens, causal: bool, compute_dtype=torch.float32):
+    """``forward_continuous_batching_fp16``.
+
+    Per batch row b only keys ``[0, min(cache_lens[b]+1, max_N))`` are read
+    (continuous_batching_kernel.cu:66-69); causal additionally masks
+    ``k_idx > cache_lens[b]`` (:122), which cannot fire inside that range, so both
+    ``causal`` values give the same result.  An empty range (cache_len < 0) gives
+    0/0 = NaN (:192).
+    """
+    b_, h_q, _, d = q.shape
+    max_n = k.shape[2]
+    k = expand_kv(k, h_q)
+    v = expand_kv(v, h_q)
+    lens = torch.as_tensor(cache_lens).to(torch.int64).cpu()
+    cur = torch.clamp(lens + 1, max=max_n)
+    idx = torch.arange(max_n).view(1, max_n)
+    mask = idx >= cur.view(-1, 1)
+    if causal:
+        mask = mask | (idx > lens.view(-1, 1))
+    return _attend(q, k, v, mask.view(b_, 1, 1, max_n), compute_dtype)
+
+
+def paged_gather(k_cache, v_cache, block_table, seq_lens, max_num_blocks):
+    """Gather the paged cache into contiguous [B,H_KV,L,D] tensors plus a length mask.
+
+    Token ``t`` of sequence ``b`` lives at page
+    ``block_table.flat[b*max_num_blocks + t/16]``, row ``t%16``, element address
+    ``((phys*H_KV + h_kv)*16 + row)*D + col`` (flash_attn_kernel.cu:3418, :3438,
+    :3446).  ``max_num_blocks`` is the row stride into the flattened table, exactly
+    as the kernel uses it.  Returns (k, v, lens) with L = max(seq_lens, 0).
+    """
+    bt = block_table.reshape(-1).to(torch.int64).cpu()
+    lens = torch.as_tensor(seq_lens).to(torch.int64).cpu()
+    b_ = lens.numel()
+    h_kv, page, d = k_cache.shape[1], k_cache.shape[2], k_cache.shape[3]
+    assert page == PAGE_BLOCK_SIZE
+    lmax = max(int(lens.max().item()), 0) if b_ else 0
+    k = torch.zeros(b_, h_kv, lmax, d, dtype=k_cache.dtype)
+    v = torch.zeros_like(k)
+    for b in range(b_):
+        n = int(lens[b])
+        if n <= 0:
+            continue
+        t = torch.arange(n)
+        phys = bt[b * max_num_blocks + t // PAGE_BLOCK_SIZE]
+        row = t % PAGE_BLOCK_SIZE
+        k[b, :, :n] = k_cache[phys, :, row].permute(1, 0, 2)
+        v[b, :, :n] = v_cache[phys, :, row].permute(1, 0, 2)
+    return k, v, lens
+
+
+def paged_decode(q, k_cache, v_cache, block_table, seq_lens, max_num_blocks,
+                 compute_dtype=torch.float32):
+    """``forward_paged_decode_gqa_fp16``: attends exactly tokens ``[0, seq_lens[b])``
+    of the paged cache (no causal argument, flash_attn_kernel.cu:3432-3490);
+    ``seq_lens[b] <= 0`` gives NaN (0/0 at :3511)."""
+    k, v, lens = paged_gather(k_cache, v_cache, block_table, seq_lens, max_num_blocks)
+    b_, h_q = q.shape[0], q.shape[1]
+    lmax = k.shape[2]
+    k = expand_kv(k, h_q)
+    v = expand_kv(v, h_q)
+    mask = torch.arange(lmax).view(1, lmax) >= lens.view(-1, 1)
+    return _attend(q, k, v, mask.view(b_, 1, 1, lmax), compute_dtype)
+
+
+def varlen_row_limit(max_seqlen: int, d: int) -> int:
+    """Number of leading rows of each sequence the reference ever writes.
+
+    The grid's x extent is ``ceil(max_seqlen / tile)`` query tiles per sequence
+    (flash_attn_kernel.cu:3319-3320 and :3336-3337) with tile 32 for D<=128 and 8
+    for D>128, so rows at local index >= ``tile*ceil(max_seqlen/tile)`` stay at the
+    zero the output was initialised with (:3382).
+    """
+    tile = VARLEN_TILE_SMALL_D if d <= MAX_D_SMALL else VARLEN_TILE_LARGE_D
+    return ((max_seqlen + tile - 1) // tile) * tile
+
+
+def varlen_prefill(q, k, v, cu_seqlens, max_seqlen: int, causal: bool,
+                   compute_dtype=torch.float32):
+    """``forward_varlen_prefill_fp16`` on packed Q/K/V [total, H, D].
+
+    Sequence b spans packed rows ``[cu[b], cu[b+1])`` (flash_attn_kernel.cu:3021-3023);
+    its queries attend only keys of the same range (:3061) and causal masks
+    ``k_idx > q_idx`` (:3087); empty or negative-length ranges are skipped (:3025,
+    :3030); rows beyond :func:`varlen_row_limit` are never written (left 0).
+    """
+    total, h, d = q.shape
+    cu = torch.as_tensor(cu_seqlens).to(torch.int64).cpu()
+    out = torch.zeros(total, h, d, dtype=compute_dtype)
+    limit = varlen_row_limit(max_seqlen, d)
+    for b in range(cu.numel() - 1):
+        s, e = int(cu[b]), int(cu[b + 1])
+        n = e - s
+        if n <= 0:
+            continue
+        rows = min(n, limit)
+        qs = q[s:s + rows].permute(1, 0, 2).unsqueeze(0)  # [1,H,rows,D]
+        ks = k[s:e].permute(1, 0, 2).unsqueeze(0)
+        vs = v[s:e].permute(1, 0, 2).unsqueeze(0)
+        mask = None
+        if causal:
+            mask = torch.arange(n).view(1, n) > torch.arange(rows).view(rows, 1)
+        o = _attend(qs, ks, vs, mask, compute_dtype)[0].permute(1, 0, 2)
+        out[s:s + rows] = o
+    return out
+
+
+def round_half_away(x: torch.Tensor) -> torch.Tensor:
+    """C ``roundf``: round half away from zero, evaluated in float64 so the
+    ``+0.5`` is exact for every float32 input."""
+    x64 = x.to(torch.float64)
+    return (torch.sign(x64) * torch.floor(torch.abs(x64) + 0.5)).to(x.dtype)
+
+
+def quantize_int8(x_f16: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """``int8 = clamp(roundf(x / s), -127, 127)`` (flash_attn_kernel.cu:2837, :2856).
+
+    The division is evaluated as ``x * (1/s)`` in float32 with ``1/s`` correctly
+    rounded: that is the reciprocal-multiply the reference's ``--use_fast_math``
+    build (setup.py:25) turns the division into, and it is what the HIP kernel
+    computes, so the integers agree exactly.  Clamping uses fmin/fmax semantics
+    (a NaN quotient becomes +127, as ``fmaxf(-127, fminf(127, NaN))`` does).
+    """
+    inv = (torch.ones_like(s, dtype=torch.float32) / s.to(torch.float32))
+    y = x_f16.to(torch.float32) * inv
+    r = round_half_away(y)
+    r = torch.fmin(torch.full_like(r, 127.0), r)
+    r = torch.fmax(torch.full_like(r, -127.0), r)
+    return r.to(torch.int32)
+
+
+def int8_k_scale_per_head(k_scale: torch.Tensor, b_: int, h_kv: int) -> torch.Tensor:
+    """The scale the reference kernel actually uses for head (b, h_kv).
+
+    The host requires ``k_scale.shape == [B, H_KV, N]`` (flash_attn_kernel.cu:2970-2971)
+    but the kernel reads ``K_scale[b*H_KV + h_kv]`` of the flattened tensor (:2825),
+    i.e. element ``b*H_KV + h_kv`` of ``k_scale.reshape(-1)``.
+    """
+    flat = k_scale.reshape(-1).to(torch.float32)
+    return flat[: b_ * h_kv].view(b_, h_kv)
+
+
+def decode_int8(q, k, v, q_scale, k_scale, cache_len: int, compute_dtype=torch.float32):
+    """``forward_decode_int8_gqa`` (flash_attn_kernel.cu:2796-2939).
+
+    1. ``qi = clamp(roundf(q/q_s))`` with ``q_s = q_scale[b, h_q]`` (:2824, :2837).
+    2. ``ki = clamp(roundf(k/k_s))`` with ``k_s`` from :func:`int8_k_scale_per_head`.
+    3. ``score = (sum_d qi*ki) * q_s * k_s * (1/sqrt(D))`` with an exact integer
+       dot (:2871-2888).
+    4. Keys ``k_idx > cache_len`` are always masked (:2866).
+    5. V stays fp16; softmax and PV in float (:2908-2921).
+    """
+    b_, h_q, _, d = q.shape
+    h_kv, n = k.shape[1], k.shape[2]
+    qs = q_scale.reshape(b_, h_q).to(torch.float32)
+    ks = int8_k_scale_per_head(k_scale, b_, h_kv)
+    qi = quantize_int8(q, qs.view(b_, h_q, 1, 1))                 # [B,H_Q,1,D]
+    ki = quantize_int8(k, ks.view(b_, h_kv, 1, 1))                # [B,H_KV,N,D]
+    ki = expand_kv(ki, h_q)
+    dots = torch.matmul(qi.to(torch.float64), ki.to(torch.float64).transpose(-1, -2))  # exact
+    ks_q = ks.repeat_interleave(h_q // h_kv, dim=1)
+    # Reference order: (float)int_dot * q_s * k_s * scale, all float32 (:2888).
+    scale = host_scale_f32(d)
+    scores = dots.to(torch.float32) * qs.view(b_, h_q, 1, 1) * ks_q.view(b_, h_q, 1, 1) * scale
+    scores = scores.to(compute_dtype)
+    mask = (torch.arange(n) > cache_len).view(1, 1, 1, n)
+    scores = scores.masked_fill(mask, float("-inf"))
+    probs = _softmax_rows(scores)
+    return torch.matmul(probs, expand_kv(v, h_q).to(compute_dtype))
+
+
+def decode_int8_dequant_reference(q, k, v, q_scale, k_scale, cache_len: int):
+    """Quantize-dequantize form of :func:`decode_int8` (float64): attention of the
+    dequantized ``qi*q_s`` against ``ki*k_s``.  Equal to :func:`decode_int8` up to
+    float rounding; used to check that restatement."""
+    b_, h_q, _, d = q.shape
+    h_kv = k.shape[1]
+    qs = q_scale.reshape(b_, h_q).to(torch.float32)
+    ks = int8_k_scale_per_head(k_scale, b_, h_kv)
+    qd = quantize_int8(q, qs.view(b_, h_q, 1, 1)).to(torch.float64) * qs.view(b_, h_q, 1, 1).double()
+    kd = quantize_int8(k, ks.view(b_, h_kv, 1, 1)).to(torch.float64) * ks.view(b_, h_kv, 1, 1).double()
+    return decode(qd, kd, v.double(), True, cache_len, compute_dtype=torch.float64)

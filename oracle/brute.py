@@ -1,0 +1,222 @@
+"""Pure-Python fp64 loop restatement of the reference kernels (TEST INFRASTRUCTURE ONLY).
+
+An independent second restatement used only to pin ``oracle/attention.py`` on
+tiny inputs.  Where ``attention.py`` writes each entry point as a closed-form
+masked softmax, this module walks the reference kernels' own loop structure:
+the launch grid (which rows get a thread at all), the KV tile loop, the
+``-FLT_MAX`` mask sentinel, the online-softmax state ``(m_i, l_i, acc)`` and the
+final ``acc / l_i`` (which is 0/0 = NaN when no key survived).  A plausible
+mistake in either restatement (a wrong mask bound, a transposed GQA map, a
+page-address slip, an off-by-one in the varlen grid) makes the two disagree.
+
+Inputs are nested Python lists or torch tensors (converted with ``.tolist()``);
+use only for shapes of a few thousand elements.
+"""
+from __future__ import annotations
+
+import math
+
+FLT_MAX = 3.4028234663852886e38
+PAGE = 16  # PAGE_BLOCK_SIZE (flash_attn_kernel.cu:3389)
+
+
+def _tolist(x):
+    return x.tolist() if hasattr(x, "tolist") else x
+
+
+def _online_attend(qvec, key_rows, val_rows, masked, scale, tile):
+    """Reference online-softmax loop over keys in tiles of ``tile``
+    (e.g. flash_attn_kernel.cu:1196-1282): per tile, masked scores are the
+    ``-FLT_MAX`` sentinel and are skipped; a tile with every score masked is
+    skipped entirely; output is ``acc / l`` (NaN when l == 0)."""
+    d = len(qvec)
+    m_i, l_i = -FLT_MAX, 0.0
+    acc = [0.0] * d
+    n = len(key_rows)
+    for start in range(0, n, tile):
+        idx = range(start, min(start + tile, n))
+        scores = []
+        for j in idx:
+            if masked(j):
+                scores.append(-FLT_MAX)
+            else:
+                scores.append(sum(qvec[t] * key_rows[j][t] for t in range(d)) * scale)
+        m_blk = max(scores) if scores else -FLT_MAX
+        if m_blk == -FLT_MAX:
+            continue
+        m_new = max(m_i, m_blk)
+        alpha = 0.0 if m_i == -FLT_MAX else math.exp(m_i - m_new)
+        w = [0.0] * d
+        beta = 0.0
+        for s, j in zip(scores, idx):
+            if s == -FLT_MAX:
+                continue
+            p = math.exp(s - m_new)
+            beta += p
+            for t in range(d):
+                w[t] += val_rows[j][t] * p
+        acc = [alpha * acc[t] + w[t] for t in range(d)]
+        l_i = alpha * l_i + beta
+        m_i = m_new
+    if l_i == 0.0:
+        return [float("nan")] * d
+    return [a / l_i for a in acc]
+
+
+def prefill(q, k, v, causal):
+    """a1/a2: grid (B*H_Q, ceil(N/32)), one query row per thread, keys 0..N-1,
+    causal masks k_idx > q_idx (flash_attn_kernel.cu:1223), GQA map :2489."""
+    q, k, v = _tolist(q), _tolist(k), _tolist(v)
+    b_, hq, n, d = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    hkv = len(k[0])
+    scale = 1.0 / math.sqrt(d)
+    out = [[[None] * n for _ in range(hq)] for _ in range(b_)]
+    for b in range(b_):
+        for h in range(hq):
+            g = h // (hq // hkv)
+            for i in range(n):
+                out[b][h][i] = _online_attend(q[b][h][i], k[b][g], v[b][g],
+                                              lambda j, i=i: causal and j > i, scale, 32)
+    return out
+
+
+def decode(q, k, v, causal, cache_len):
+    """a3/a4: one (b, h_q) per block, keys 0..N-1 in tiles of 64, causal masks
+    k_idx > cache_len (flash_attn_kernel.cu:1719)."""
+    q, k, v = _tolist(q), _tolist(k), _tolist(v)
+    b_, hq, d = len(q), len(q[0]), len(q[0][0][0])
+    hkv = len(k[0])
+    scale = 1.0 / math.sqrt(d)
+    out = [[None] * hq for _ in range(b_)]
+    for b in range(b_):
+        for h in range(hq):
+            g = h // (hq // hkv)
+            out[b][h] = [_online_attend(q[b][h][0], k[b][g], v[b][g],
+                                        lambda j: causal and j > cache_len, scale, 64)]
+    return out
+
+
+def continuous_batching(q, k, v, cache_lens, causal):
+    """a5: current_N = min(cache_len+1, max_N) rows read (continuous_batching_kernel.cu:66-69),
+    causal masks k_idx > cache_len (:122)."""
+    q, k, v, cl = _tolist(q), _tolist(k), _tolist(v), _tolist(cache_lens)
+    b_, hq, d = len(q), len(q[0]), len(q[0][0][0])
+    hkv, max_n = len(k[0]), len(k[0][0])
+    scale = 1.0 / math.sqrt(d)
+    out = [[None] * hq for _ in range(b_)]
+    for b in range(b_):
+        c = cl[b]
+        cur = min(c + 1, max_n)
+        for h in range(hq):
+            g = h // (hq // hkv)
+            rows_k = k[b][g][:max(cur, 0)]
+            rows_v = v[b][g][:max(cur, 0)]
+            out[b][h] = [_online_attend(q[b][h][0], rows_k, rows_v,
+                                        lambda j, c=c: causal and j > c, scale, 64)]
+    return out
+
+
+def paged_decode(q, k_cache, v_cache, block_table, seq_lens, max_num_blocks):
+    """a7: page loop with physical = block_table[b*max_num_blocks + i]
+    (flash_attn_kernel.cu:3438), element ((phys*H_KV + h_kv)*16 + row)*D + col
+    computed on the flattened cache (:3418, :3446)."""
+    q = _tolist(q)
+    bt = [x for row in _tolist(block_table) for x in row]
+    sl = _tolist(seq_lens)
+    kc, vc = k_cache.reshape(-1).tolist(), v_cache.reshape(-1).tolist()
+    hkv, d = k_cache.shape[1], k_cache.shape[3]
+    b_, hq = len(q), len(q[0])
+    scale = 1.0 / math.sqrt(d)
+    out = [[None] * hq for _ in range(b_)]
+    for b in range(b_):
+        n = sl[b]
+        for h in range(hq):
+            g = h // (hq // hkv)
+            rows_k, rows_v = [], []
+            for t in range(max(n, 0)):
+                phys = bt[b * max_num_blocks + t // PAGE]
+                base = ((phys * hkv + g) * PAGE + t % PAGE) * d
+                rows_k.append(kc[base:base + d])
+                rows_v.append(vc[base:base + d])
+            out[b][h] = [_online_attend(q[b][h][0], rows_k, rows_v, lambda j: False, scale, PAGE)]
+    return out
+
+
+def varlen_prefill(q, k, v, cu_seqlens, max_seqlen, causal):
+    """a6: grid (ceil(max_seqlen/T), H, batch) with T = 32 (D<=128) or 8 (D>128)
+    (flash_attn_kernel.cu:3319-3338); thread rows q_start+tid inside [cu[b], cu[b+1]);
+    keys of the same sequence; causal k_idx > q_idx in packed coordinates (:3087).
+    Rows never visited keep the output's initial zeros (:3382)."""
+    q, k, v, cu = _tolist(q), _tolist(k), _tolist(v), _tolist(cu_seqlens)
+    total, h_, d = len(q), len(q[0]), len(q[0][0])
+    tile = 32 if d <= 128 else 8
+    scale = 1.0 / math.sqrt(d)
+    out = [[[0.0] * d for _ in range(h_)] for _ in range(total)]
+    n_tiles = (max_seqlen + tile - 1) // tile
+    for b in range(len(cu) - 1):
+        s, e = cu[b], cu[b + 1]
+        if e - s == 0:
+            continue
+        for h in range(h_):
+            keys = [k[r][h] for r in range(s, e)] if e > s else []
+            vals = [v[r][h] for r in range(s, e)] if e > s else []
+            for t in range(n_tiles):
+                for tid in range(tile):
+                    qi = s + t * tile + tid
+                    if qi >= e:
+                        continue
+                    out[qi][h] = _online_attend(q[qi][h], keys, vals,
+                                                lambda j, qi=qi: causal and (s + j) > qi, scale, 32)
+    return out
+
+
+def _roundf(x):
+    """C roundf (half away from zero)."""
+    return math.copysign(math.floor(abs(x) + 0.5), x)
+
+
+def _quant(x, inv):
+    y = x * inv
+    if y != y:  # NaN: fminf(127, NaN) = 127, fmaxf(-127, 127) = 127
+        return 127
+    return int(max(-127.0, min(127.0, _roundf(y))))
+
+
+def decode_int8(q, k, v, q_scale, k_scale, cache_len):
+    """a8 (flash_attn_kernel.cu:2796-2939): integer dot of clamp(roundf(x*inv_s))
+    codes, score = dot*q_s*k_s*scale (:2888), k_s = k_scale.flat[b*H_KV+h_kv]
+    (:2825), keys k_idx > cache_len always masked (:2866), V in fp16.
+    ``inv_s`` is the float32 reciprocal of the scale (see oracle.attention.quantize_int8)."""
+    import numpy as np
+
+    q, k, v = _tolist(q), _tolist(k), _tolist(v)
+    qs = q_scale.reshape(-1).tolist()
+    ks_flat = k_scale.reshape(-1).tolist()
+    b_, hq, d = len(q), len(q[0]), len(q[0][0][0])
+    hkv = len(k[0])
+    f32 = np.float32
+    scale = f32(1.0) / np.sqrt(f32(d))  # 1.0f / std::sqrt((float)D) (flash_attn_kernel.cu:2983)
+    out = [[None] * hq for _ in range(b_)]
+    for b in range(b_):
+        for h in range(hq):
+            g = h // (hq // hkv)
+            q_s = f32(qs[b * hq + h])
+            k_s = f32(ks_flat[b * hkv + g])
+            inv_q = float(f32(1.0) / q_s)
+            inv_k = float(f32(1.0) / k_s)
+            qi = [_quant(float(f32(x) * f32(inv_q)), 1.0) for x in q[b][h][0]]
+            n = len(k[b][g])
+            rows = []
+            for j in range(n):
+                kj = [_quant(float(f32(x) * f32(inv_k)), 1.0) for x in k[b][g][j]]
+                rows.append(kj)
+            # scores in float32 in the reference's multiplication order
+            sc = []
+            for j in range(n):
+                dot = sum(a * c for a, c in zip(qi, rows[j]))
+                sc.append(float(f32(dot) * q_s * k_s * scale))
+            m = max(sc[j] for j in range(n) if j <= cache_len)
+            p = [math.exp(sc[j] - m) if j <= cache_len else 0.0 for j in range(n)]
+            l_ = sum(p)
+            out[b][h] = [[sum(p[j] * v[b][g][j][t] for j in range(n)) / l_ for t in range(d)]]
+    return out

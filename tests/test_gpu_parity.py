@@ -1,0 +1,407 @@
+"""GPU parity: every hot-path entry point of ``flash_attn_v100`` against the CPU oracle.
+
+Shapes, seeds and cases follow the reference's own test scripts (test.py,
+test_decode.py, test_gqa.py, test_wmma.py, test_prefill_gqa.py,
+test_continuous_batching.py, test_async.py) plus the BASELINE configs, edge
+cases (cache_len 0 and N-1, ragged tails, D not a multiple of 8/16, empty
+ranges -> NaN) and full-size configs checked on sampled sequences.
+Tolerance: max-abs 2e-3 + rtol 1e-2 (fp16 paths), rel-L2 1.5e-2 (INT8).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import attention as A
+from tests.helpers import INT8_REL_L2, assert_close, randn, rel_l2
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def cuda(*ts):
+    return [t.to(DEV).contiguous() for t in ts]
+
+
+# ---------------------------------------------------------------- prefill
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_fp16_config1(fa, causal):
+    """BASELINE config 1 / test.py:18-57: B=2,H=8,N=256,D=64, seed 0."""
+    g = gen(0)
+    q, k, v = randn(g, 2, 8, 256, 64), randn(g, 2, 8, 256, 64), randn(g, 2, 8, 256, 64)
+    out = fa.forward_fp16(*cuda(q, k, v), causal)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16 and out.shape == q.shape
+    assert_close(out, A.prefill(q, k, v, causal), what="forward_fp16 cfg1")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,n,d", [
+    (1, 2, 1, 64), (1, 2, 5, 64), (2, 3, 33, 64), (1, 2, 127, 128), (1, 2, 129, 128),
+    (1, 4, 300, 128), (1, 2, 77, 32), (1, 2, 70, 80), (1, 2, 50, 96), (1, 2, 45, 36),
+    (1, 2, 130, 256), (1, 1, 65, 200), (1, 2, 64, 16),
+])
+def test_forward_fp16_shapes(fa, causal, b, h, n, d):
+    g = gen(n * 7 + d)
+    q, k, v = randn(g, b, h, n, d), randn(g, b, h, n, d), randn(g, b, h, n, d)
+    out = fa.forward_fp16(*cuda(q, k, v), causal)
+    assert_close(out, A.prefill(q, k, v, causal), what=f"forward_fp16 {b,h,n,d}")
+
+
+@pytest.mark.parametrize("b,h,n,d", [(1, 4, 64, 64), (2, 4, 128, 64), (1, 8, 256, 64),
+                                     (2, 8, 512, 64), (1, 4, 128, 128), (1, 2, 96, 32)])
+def test_forward_fp16_wmma(fa, b, h, n, d):
+    """test_wmma.py:25-78 (seed 42): WMMA name == forward_fp16 == oracle."""
+    g = gen(42)
+    q, k, v = randn(g, b, h, n, d), randn(g, b, h, n, d), randn(g, b, h, n, d)
+    qc, kc, vc = cuda(q, k, v)
+    out = fa.forward_fp16_wmma(qc, kc, vc, True)
+    ref = fa.forward_fp16(qc, kc, vc, True)
+    assert_close(out, A.prefill(q, k, v, True), what="wmma")
+    assert torch.equal(out, ref)
+
+
+def test_forward_fp16_wmma_rejects_unsupported_d(fa):
+    x = torch.zeros(1, 1, 8, 72, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        fa.forward_fp16_wmma(x, x, x, True)
+    y = torch.zeros(1, 1, 8, 144, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        fa.forward_fp16_wmma(y, y, y, True)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,hq,hkv,n,d", [(1, 8, 4, 64, 64), (2, 16, 4, 96, 64), (1, 32, 8, 128, 128),
+                                          (1, 32, 8, 64, 256)])
+def test_prefill_gqa(fa, causal, b, hq, hkv, n, d):
+    """test_gqa.py:133-167 shapes (seed 1234), plus _out aliasing (test.py:108-131)."""
+    g = gen(1234)
+    q, k, v = randn(g, b, hq, n, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+    qc, kc, vc = cuda(q, k, v)
+    ref = A.prefill(q, k, v, causal)
+    assert_close(fa.forward_prefill_gqa_fp16(qc, kc, vc, causal), ref, what="prefill_gqa")
+    assert_close(fa.forward_prefill_gqa_fp16_warp(qc, kc, vc, causal), ref, what="prefill_gqa_warp")
+    out = torch.empty_like(qc)
+    ret = fa.forward_prefill_gqa_fp16_out(out, qc, kc, vc, causal)
+    assert ret.data_ptr() == out.data_ptr()
+    assert_close(out, ref, what="prefill_gqa_out")
+
+
+def test_prefill_mha_equals_gqa_api(fa):
+    """test_prefill_gqa.py:94-116: with H_Q == H_KV the GQA API equals forward_fp16."""
+    g = gen(42)
+    q, k, v = cuda(randn(g, 2, 4, 100, 64), randn(g, 2, 4, 100, 64), randn(g, 2, 4, 100, 64))
+    a = fa.forward_fp16(q, k, v, True)
+    b = fa.forward_prefill_gqa_fp16(q, k, v, True)
+    assert (a.float() - b.float()).abs().max().item() <= 1e-3
+
+
+# ---------------------------------------------------------------- decode
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,n,d,cache_len", [(2, 4, 1, 64, 0), (1, 8, 65, 64, 0), (2, 8, 65, 64, 64),
+                                               (1, 8, 300, 128, 200), (1, 2, 40, 256, 39),
+                                               (1, 2, 33, 72, 10), (1, 1, 5000, 128, 4999)])
+def test_forward_decode_fp16(fa, causal, b, h, n, d, cache_len):
+    """test_decode.py:218-266: MHA decode, causal masks k > cache_len."""
+    g = gen(b * 1000 + n + d)
+    q, k, v = randn(g, b, h, 1, d), randn(g, b, h, n, d), randn(g, b, h, n, d)
+    out = fa.forward_decode_fp16(*cuda(q, k, v), causal, cache_len)
+    assert_close(out, A.decode(q, k, v, causal, cache_len), what="decode_fp16")
+
+
+@pytest.mark.parametrize("b,hq,hkv,n,d", [(1, 8, 4, 65, 64), (2, 16, 4, 127, 64), (1, 32, 8, 257, 128),
+                                          (1, 32, 8, 129, 256), (2, 12, 4, 70, 128), (1, 64, 2, 500, 64),
+                                          (3, 6, 1, 1000, 96)])
+def test_forward_decode_gqa_fp16(fa, b, hq, hkv, n, d):
+    """test_gqa.py:120-153 shapes (seed 1234) plus non-power-of-two group sizes."""
+    g = gen(1234)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+    qc, kc, vc = cuda(q, k, v)
+    for causal, cl in ((True, n - 1), (True, n // 2), (False, n // 3)):
+        out = fa.forward_decode_gqa_fp16(qc, kc, vc, causal, cl)
+        assert_close(out, A.decode(q, k, v, causal, cl), what=f"decode_gqa c={causal} cl={cl}")
+
+
+def test_decode_gqa_config2(fa):
+    """Q [1,32,1,128], K/V [1,8,4097,128], cache_len 4096, causal."""
+    g = gen(0)
+    q, k, v = randn(g, 1, 32, 1, 128), randn(g, 1, 8, 4097, 128), randn(g, 1, 8, 4097, 128)
+    out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, 4096)
+    assert_close(out, A.decode(q, k, v, True, 4096), what="config2")
+
+
+def test_decode_gqa_out_and_stream(fa):
+    """_out writes into the caller's tensor; _stream equals the default (test_async.py:37-65)."""
+    g = gen(7)
+    q, k, v = cuda(randn(g, 2, 8, 1, 64), randn(g, 2, 2, 600, 64), randn(g, 2, 2, 600, 64))
+    ref = fa.forward_decode_gqa_fp16(q, k, v, True, 0)
+    out = torch.empty_like(q)
+    ret = fa.forward_decode_gqa_fp16_out(out, q, k, v, True, 0)
+    assert ret.data_ptr() == out.data_ptr()
+    assert torch.equal(out, ref)
+    assert_close(ref, A.decode(q.cpu(), k.cpu(), v.cpu(), True, 0), what="cache_len=0")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    got = fa.forward_decode_gqa_fp16_stream(q, k, v, True, 599, s.cuda_stream)
+    s.synchronize()
+    assert torch.equal(got, fa.forward_decode_gqa_fp16(q, k, v, True, 599))
+
+
+def test_decode_validation_errors(fa):
+    """test.py:70-102, :133-139: errors surface as RuntimeError."""
+    q = torch.zeros(1, 4, 1, 64, dtype=torch.float16, device=DEV)
+    k = torch.zeros(1, 2, 10, 64, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_gqa_fp16(q, k.float(), k, True, 3)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_gqa_fp16(q, k, k, True, -1)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_gqa_fp16(q, k, k, True, 10)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_gqa_fp16(q, k.cpu(), k, True, 3)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_gqa_fp16_out(torch.empty(1, 4, 2, 64, dtype=torch.float16, device=DEV), q, k, k, True, 3)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_fp16(q, k, k, True, 3)  # MHA API needs equal head counts
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_gqa_fp16(q, k[:, :, ::2], k[:, :, ::2], True, 3)  # non-contiguous
+
+
+# ---------------------------------------------------------------- continuous batching
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,hq,hkv,d,max_n,cls", [
+    (3, 8, 2, 64, 17, [0, 3, 15]), (2, 32, 8, 256, 33, [0, 31]),      # test_continuous_batching.py:349-352
+    (4, 32, 8, 128, 1025, [16, 1024, 500, 2000]), (5, 4, 4, 96, 700, [0, 699, 1, 350, 64]),
+])
+def test_continuous_batching(fa, causal, b, hq, hkv, d, max_n, cls):
+    g = gen(0)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, max_n, d), randn(g, b, hkv, max_n, d)
+    cl = torch.tensor(cls, dtype=torch.int32)
+    out = fa.forward_continuous_batching_fp16(*cuda(q, k, v, cl), causal)
+    assert_close(out, A.continuous_batching(q, k, v, cl, causal), what="cb")
+
+
+def test_continuous_batching_negative_len_is_nan(fa):
+    g = gen(1)
+    q, k, v = randn(g, 2, 4, 1, 64), randn(g, 2, 2, 300, 64), randn(g, 2, 2, 300, 64)
+    cl = torch.tensor([-1, 100], dtype=torch.int32)
+    out = fa.forward_continuous_batching_fp16(*cuda(q, k, v, cl), True)
+    assert torch.isnan(out[0].float()).all()
+    assert_close(out, A.continuous_batching(q, k, v, cl, True), what="cb nan")
+
+
+def _sample_check_decode_like(out, ref_fn, rows):
+    for b in rows:
+        assert_close(out[b:b + 1], ref_fn(b), what=f"row {b}")
+
+
+def test_continuous_batching_config3_sampled(fa):
+    """BASELINE config 3 at full size (B=64, 32:8 heads, max_N=8193, D=128), cache_lens
+    U[16,8192]; every sequence's output is checked against the oracle on that sequence."""
+    g = gen(3)
+    B, HQ, HKV, MAXN, D = 64, 32, 8, 8193, 128
+    cl = torch.randint(16, 8193, (B,), generator=g, dtype=torch.int32)
+    gg = torch.Generator(device=DEV).manual_seed(3)
+    q = torch.randn(B, HQ, 1, D, generator=gg, device=DEV).half()
+    k = torch.randn(B, HKV, MAXN, D, generator=gg, device=DEV).half()
+    v = torch.randn(B, HKV, MAXN, D, generator=gg, device=DEV).half()
+    out = fa.forward_continuous_batching_fp16(q, k, v, cl.to(DEV), True).cpu()
+    for b in range(0, B, 5):
+        n = min(int(cl[b]) + 1, MAXN)
+        ref = A.decode(q[b:b + 1].cpu(), k[b:b + 1, :, :n].cpu(), v[b:b + 1, :, :n].cpu(), True, n - 1)
+        assert_close(out[b:b + 1], ref, what=f"cfg3 b={b}")
+
+
+# ---------------------------------------------------------------- paged decode
+
+def build_paged(k, v, seq_lens, order, page=16):
+    """Reference layout builder (test_decode.py:22-44)."""
+    B, HKV, _, D = k.shape
+    mnb = max((s + page - 1) // page for s in seq_lens)
+    npages = max(order[: sum((s + page - 1) // page for s in seq_lens)]) + 1
+    kc = torch.zeros(npages, HKV, page, D, dtype=k.dtype)
+    vc = torch.zeros_like(kc)
+    bt = torch.full((B, mnb), -1, dtype=torch.int32)
+    cur = 0
+    for b, s in enumerate(seq_lens):
+        for blk in range((s + page - 1) // page):
+            p = order[cur]
+            cur += 1
+            bt[b, blk] = p
+            st, en = blk * page, min(blk * page + page, s)
+            kc[p, :, : en - st] = k[b, :, st:en]
+            vc[p, :, : en - st] = v[b, :, st:en]
+    return kc, vc, bt, mnb
+
+
+def test_paged_decode_reference_case(fa):
+    """test_decode.py:269-322: seed 2025, seq_lens [16,23,33], pages [5,2,7,1,9,3],
+    then a cache update must change the output and still match."""
+    g = gen(2025)
+    B, HQ, HKV, D = 3, 8, 4, 64
+    sl = [16, 23, 33]
+    q, k, v = randn(g, B, HQ, 1, D), randn(g, B, HKV, 33, D), randn(g, B, HKV, 33, D)
+    order = [5, 2, 7, 1, 9, 3]
+    kc, vc, bt, mnb = build_paged(k, v, sl, order)
+    slt = torch.tensor(sl, dtype=torch.int32)
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), mnb)
+    ref = A.paged_decode(q, kc, vc, bt, slt, mnb)
+    assert_close(out, ref, what="paged ref case")
+    k2, v2 = k.clone(), v.clone()
+    k2[1, :, 16:23] += 0.5
+    v2[1, :, 16:23] -= 0.25
+    kc2, vc2, _, _ = build_paged(k2, v2, sl, order)
+    out2 = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc2, vc2, bt, slt), mnb)
+    assert_close(out2, A.paged_decode(q, kc2, vc2, bt, slt, mnb), what="paged updated")
+    assert (out2.float() - out.float()).abs().max().item() > 1e-4
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (8, 8, 64), (16, 2, 256), (12, 4, 80)])
+def test_paged_decode_random_tables(fa, hq, hkv, d):
+    g = gen(hq + d)
+    B = 6
+    sl = [1, 15, 16, 17, 300, 1000]
+    mnb = 64
+    npages = 200
+    perm = torch.randperm(npages, generator=g)
+    bt = torch.full((B, mnb), -1, dtype=torch.int32)
+    cur = 0
+    for b, s in enumerate(sl):
+        nb = (s + 15) // 16
+        bt[b, :nb] = perm[cur:cur + nb].int()
+        cur += nb
+    kc, vc = randn(g, npages, hkv, 16, d), randn(g, npages, hkv, 16, d)
+    q = randn(g, B, hq, 1, d)
+    slt = torch.tensor(sl, dtype=torch.int32)
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), mnb)
+    assert_close(out, A.paged_decode(q, kc, vc, bt, slt, mnb), what="paged random")
+
+
+def test_paged_decode_empty_sequence_is_nan(fa):
+    g = gen(5)
+    q, kc, vc = randn(g, 2, 4, 1, 64), randn(g, 4, 2, 16, 64), randn(g, 4, 2, 16, 64)
+    bt = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32)
+    slt = torch.tensor([0, 20], dtype=torch.int32)
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), 2)
+    assert torch.isnan(out[0].float()).all()
+    assert_close(out, A.paged_decode(q, kc, vc, bt, slt, 2), what="paged nan")
+
+
+def test_paged_decode_config4_sampled(fa):
+    """BASELINE config 4 at full size: B=128, 32:8 heads, D=128, 65536 pages,
+    seq_lens U[64,4096], block_table = first 32768 entries of randperm(65536)."""
+    g = gen(4)
+    B, HQ, HKV, D, P, MNB = 128, 32, 8, 128, 65536, 256
+    sl = torch.randint(64, 4097, (B,), generator=g, dtype=torch.int32)
+    bt = torch.randperm(P, generator=g)[: B * MNB].view(B, MNB).int()
+    gg = torch.Generator(device=DEV).manual_seed(4)
+    q = torch.randn(B, HQ, 1, D, generator=gg, device=DEV).half()
+    kc = torch.randn(P, HKV, 16, D, generator=gg, device=DEV).half()
+    vc = torch.randn(P, HKV, 16, D, generator=gg, device=DEV).half()
+    out = fa.forward_paged_decode_gqa_fp16(q, kc, vc, bt.to(DEV), sl.to(DEV), MNB).cpu()
+    for b in range(0, B, 9):
+        n = int(sl[b])
+        pages = bt[b, : (n + 15) // 16].long().to(DEV)
+        kk = kc[pages].permute(1, 0, 2, 3).reshape(1, HKV, -1, D)[:, :, :n].cpu()
+        vv = vc[pages].permute(1, 0, 2, 3).reshape(1, HKV, -1, D)[:, :, :n].cpu()
+        assert_close(out[b:b + 1], A.decode(q[b:b + 1].cpu(), kk, vv, False, 0), what=f"cfg4 b={b}")
+
+
+# ---------------------------------------------------------------- varlen prefill
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("lens,h,d,max_seqlen", [
+    ([64, 128, 256], 4, 64, None), ([32, 64, 96], 8, 256, None),     # test_async.py:68-113
+    ([5, 0, 200, 37, 1], 2, 128, None), ([100, 300], 2, 64, 40),    # empty seq, row limit
+    ([70, 20], 2, 200, 30), ([129, 64, 3], 3, 80, None),
+])
+def test_varlen_prefill(fa, causal, lens, h, d, max_seqlen):
+    g = gen(sum(lens) + d)
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32)
+    tot = int(cu[-1])
+    q, k, v = randn(g, tot, h, d), randn(g, tot, h, d), randn(g, tot, h, d)
+    ms = max(lens) if max_seqlen is None else max_seqlen
+    out = fa.forward_varlen_prefill_fp16(*cuda(q, k, v, cu), ms, causal)
+    assert_close(out, A.varlen_prefill(q, k, v, cu, ms, causal), what="varlen")
+
+
+def test_varlen_equals_per_sequence_prefill_and_stream(fa):
+    g = gen(11)
+    lens = [300, 17, 512]
+    cu = torch.tensor([0, 300, 317, 829], dtype=torch.int32)
+    q, k, v = cuda(randn(g, 829, 4, 128), randn(g, 829, 4, 128), randn(g, 829, 4, 128))
+    cuc = cu.to(DEV)
+    out = fa.forward_varlen_prefill_fp16(q, k, v, cuc, 512, True)
+    for i, n in enumerate(lens):
+        s = int(cu[i])
+        seg = fa.forward_fp16(*[t[s:s + n].permute(1, 0, 2).unsqueeze(0).contiguous() for t in (q, k, v)], True)
+        assert (seg[0].permute(1, 0, 2).float() - out[s:s + n].float()).abs().max().item() <= 1e-3
+    st = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    got = fa.forward_varlen_prefill_fp16_stream(q, k, v, cuc, 512, True, st.cuda_stream)
+    st.synchronize()
+    assert torch.equal(got, out)
+
+
+def test_varlen_config5a_sampled(fa):
+    """BASELINE config 5a: 16 sequences with L ~ U[128,2048], H=32, D=128, causal."""
+    g = gen(5)
+    lens = torch.randint(128, 2049, (16,), generator=g).tolist()
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32)
+    tot = int(cu[-1])
+    gg = torch.Generator(device=DEV).manual_seed(5)
+    q, k, v = [torch.randn(tot, 32, 128, generator=gg, device=DEV).half() for _ in range(3)]
+    out = fa.forward_varlen_prefill_fp16(q, k, v, cu.to(DEV), max(lens), True).cpu()
+    for i in (0, 7, 15):
+        s, n = int(cu[i]), lens[i]
+        ref = A.prefill(*[t[s:s + n, :8].permute(1, 0, 2).unsqueeze(0).cpu() for t in (q, k, v)], True)
+        assert_close(out[s:s + n, :8], ref[0].permute(1, 0, 2), what=f"cfg5a seq {i}")
+
+
+# ---------------------------------------------------------------- INT8 decode
+
+def int8_scales(q, k):
+    B, HKV, N = k.shape[0], k.shape[1], k.shape[2]
+    qs = (q.float().abs().amax(-1).squeeze(-1) / 127).contiguous()
+    ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(B, HKV, N).contiguous()
+    return qs, ks
+
+
+@pytest.mark.parametrize("b,hq,hkv,n,d,cl", [(2, 8, 4, 65, 64, 64), (1, 32, 8, 300, 128, 150),
+                                             (2, 4, 4, 100, 128, 0), (1, 16, 2, 700, 256, 699),
+                                             (1, 6, 2, 90, 40, 50)])
+def test_decode_int8(fa, b, hq, hkv, n, d, cl):
+    g = gen(n + d)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+    qs, ks = int8_scales(q, k)
+    out = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), cl)
+    ref = A.decode_int8(q, k, v, qs, ks, cl)
+    assert rel_l2(out, ref) <= INT8_REL_L2
+    assert_close(out, ref, what="int8")  # the integer codes agree exactly, so fp16 tolerance holds too
+
+
+def test_decode_int8_k_scale_flat_quirk(fa):
+    g = gen(9)
+    q, k, v = randn(g, 2, 4, 1, 64), randn(g, 2, 2, 50, 64), randn(g, 2, 2, 50, 64)
+    qs, _ = int8_scales(q, k)
+    ks = (torch.rand(2, 2, 50, generator=g) * 0.03 + 0.02).contiguous()
+    out = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), 49)
+    assert_close(out, A.decode_int8(q, k, v, qs, ks, 49), what="int8 quirk")
+
+
+def test_decode_int8_config5b_sampled(fa):
+    """BASELINE config 5b: Q [16,32,1,128], K/V [16,8,2049,128], per-head absmax/127 scales."""
+    g = gen(55)
+    q, k, v = randn(g, 16, 32, 1, 128), randn(g, 16, 8, 2049, 128), randn(g, 16, 8, 2049, 128)
+    qs, ks = int8_scales(q, k)
+    out = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), 2048).cpu()
+    ref = A.decode_int8(q, k, v, qs, ks, 2048)
+    assert rel_l2(out, ref) <= INT8_REL_L2
+    assert_close(out, ref, what="cfg5b")

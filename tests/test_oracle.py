@@ -1,0 +1,280 @@
+"""Pins the CPU oracle (oracle/attention.py) before it is trusted as the checker.
+
+Each oracle function is checked against
+  * the independent fp64 loop restatement of the reference kernels (oracle/brute.py),
+  * closed forms that the mathematics fixes (cache_len=0, identical keys,
+    a dominant key, exactly representable INT8 codes, roundf ties),
+  * invariants between entry points (GQA == expanded MHA, paged == gathered
+    contiguous decode, varlen == per-segment prefill, continuous batching ==
+    per-row decode on the truncated cache),
+  * the committed fixtures in tests/golden/ (written by tests/golden/make_golden.py
+    from the brute-force restatement).
+The reference ships no golden vectors of its own (its tests compare against
+torch on the same GPU), so these are the pins.
+"""
+import os
+
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import brute as Bt
+from tests.helpers import randn
+
+F64 = torch.float64
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def t64(x):
+    return torch.tensor(x, dtype=F64)
+
+
+def close(a, b, tol=1e-9):
+    a, b = torch.as_tensor(a, dtype=F64), torch.as_tensor(b, dtype=F64)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    assert torch.equal(torch.isnan(a), torch.isnan(b))
+    m = ~torch.isnan(a)
+    if m.any():
+        assert (a[m] - b[m]).abs().max().item() < tol
+
+
+# ---------------------------------------------------------------- vs brute force
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("hq,hkv,n,d", [(2, 2, 7, 8), (4, 2, 5, 8), (4, 1, 33, 4)])
+def test_prefill_vs_brute(causal, hq, hkv, n, d):
+    g = torch.Generator().manual_seed(1)
+    q, k, v = randn(g, 2, hq, n, d), randn(g, 2, hkv, n, d), randn(g, 2, hkv, n, d)
+    close(A.prefill(q, k, v, causal, F64), t64(Bt.prefill(q.double(), k.double(), v.double(), causal)))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("cache_len", [0, 5, 69])
+def test_decode_vs_brute(causal, cache_len):
+    g = torch.Generator().manual_seed(2)
+    q, k, v = randn(g, 2, 4, 1, 8), randn(g, 2, 2, 70, 8), randn(g, 2, 2, 70, 8)
+    close(A.decode(q, k, v, causal, cache_len, F64),
+          t64(Bt.decode(q.double(), k.double(), v.double(), causal, cache_len)))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_continuous_batching_vs_brute(causal):
+    g = torch.Generator().manual_seed(3)
+    q, k, v = randn(g, 5, 4, 1, 8), randn(g, 5, 2, 17, 8), randn(g, 5, 2, 17, 8)
+    cl = torch.tensor([0, 3, 15, 40, -1], dtype=torch.int32)  # last: empty range -> NaN
+    ref = t64(Bt.continuous_batching(q.double(), k.double(), v.double(), cl, causal))
+    out = A.continuous_batching(q, k, v, cl, causal, F64)
+    close(out, ref)
+    assert torch.isnan(out[4]).all() and not torch.isnan(out[:4]).any()
+
+
+def _paged_case(seed=2025, seq_lens=(16, 23, 33), order=(5, 2, 7, 1, 9, 3), hq=8, hkv=4, d=16):
+    """The reference's paged test layout (test_decode.py:22-44, :269-297)."""
+    g = torch.Generator().manual_seed(seed)
+    b = len(seq_lens)
+    lmax = max(seq_lens)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, lmax, d), randn(g, b, hkv, lmax, d)
+    mnb = max((s + 15) // 16 for s in seq_lens)
+    npages = max(order) + 1
+    kc = torch.zeros(npages, hkv, 16, d, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+    bt = torch.full((b, mnb), -1, dtype=torch.int32)
+    cur = 0
+    for i, s in enumerate(seq_lens):
+        for blk in range((s + 15) // 16):
+            p = order[cur]
+            cur += 1
+            bt[i, blk] = p
+            st, en = blk * 16, min(blk * 16 + 16, s)
+            kc[p, :, : en - st] = k[i, :, st:en]
+            vc[p, :, : en - st] = v[i, :, st:en]
+    return q, k, v, kc, vc, bt, torch.tensor(seq_lens, dtype=torch.int32), mnb
+
+
+def test_paged_vs_brute_and_contiguous():
+    q, k, v, kc, vc, bt, sl, mnb = _paged_case()
+    out = A.paged_decode(q, kc, vc, bt, sl, mnb, F64)
+    close(out, t64(Bt.paged_decode(q.double(), kc.double(), vc.double(), bt, sl, mnb)))
+    # invariant: paged == contiguous decode on each sequence's first seq_len keys
+    for i, s in enumerate(sl.tolist()):
+        ref = A.decode(q[i:i + 1], k[i:i + 1, :, :s], v[i:i + 1, :, :s], False, 0, F64)
+        close(out[i:i + 1], ref)
+
+
+def test_paged_empty_sequence_is_nan():
+    q, k, v, kc, vc, bt, sl, mnb = _paged_case()
+    sl = torch.tensor([16, 0, 33], dtype=torch.int32)
+    out = A.paged_decode(q, kc, vc, bt, sl, mnb, F64)
+    assert torch.isnan(out[1]).all() and not torch.isnan(out[0]).any()
+    close(out, t64(Bt.paged_decode(q.double(), kc.double(), vc.double(), bt, sl, mnb)))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("d,max_seqlen", [(8, 40), (8, 20), (136, 20)])
+def test_varlen_vs_brute(causal, d, max_seqlen):
+    """max_seqlen below the longest sequence exercises the rows-never-written rule:
+    D<=128 covers 32*ceil(max_seqlen/32) rows, D>128 covers 8*ceil(max_seqlen/8)."""
+    g = torch.Generator().manual_seed(4)
+    lens = [5, 0, 37, 12]
+    cu = torch.tensor([0] + list(torch.cumsum(torch.tensor(lens), 0).tolist()), dtype=torch.int32)
+    tot = int(cu[-1])
+    q, k, v = randn(g, tot, 2, d), randn(g, tot, 2, d), randn(g, tot, 2, d)
+    out = A.varlen_prefill(q, k, v, cu, max_seqlen, causal, F64)
+    close(out, t64(Bt.varlen_prefill(q.double(), k.double(), v.double(), cu, max_seqlen, causal)))
+    limit = A.varlen_row_limit(max_seqlen, d)
+    assert limit == (32 * ((max_seqlen + 31) // 32) if d <= 128 else 8 * ((max_seqlen + 7) // 8))
+    s37 = int(cu[2])
+    if limit < 37:
+        assert (out[s37 + limit:s37 + 37] == 0).all()
+    # rows that are written equal per-segment prefill
+    for i, n in enumerate(lens):
+        if n == 0:
+            continue
+        s = int(cu[i])
+        r = min(n, limit)
+        seg = A.prefill(q[s:s + n].permute(1, 0, 2)[None], k[s:s + n].permute(1, 0, 2)[None],
+                        v[s:s + n].permute(1, 0, 2)[None], causal, F64)[0].permute(1, 0, 2)
+        close(out[s:s + r], seg[:r])
+
+
+def _int8_inputs(seed=5, b=2, hq=4, hkv=2, n=9, d=16):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+    qs = q.float().abs().amax(-1).squeeze(-1) / 127
+    ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(b, hkv, n).contiguous()
+    return q, k, v, qs, ks
+
+
+@pytest.mark.parametrize("cache_len", [0, 4, 8])
+def test_int8_vs_brute_and_dequant(cache_len):
+    q, k, v, qs, ks = _int8_inputs()
+    out = A.decode_int8(q, k, v, qs, ks, cache_len, F64)
+    close(out, t64(Bt.decode_int8(q, k.float(), v.double(), qs, ks, cache_len)), tol=1e-6)
+    close(out, A.decode_int8_dequant_reference(q, k, v, qs, ks, cache_len), tol=1e-5)
+
+
+def test_int8_k_scale_flat_read_quirk():
+    """The kernel reads k_scale.flat[b*H_KV + h_kv] (flash_attn_kernel.cu:2825), not
+    k_scale[b, h_kv, 0]: a per-(b,h) scale laid out along N changes the result."""
+    q, k, v, qs, _ = _int8_inputs(n=9)
+    b, hkv, n = 2, 2, 9
+    ks = torch.rand(b, hkv, n, generator=torch.Generator().manual_seed(9)) * 0.05 + 0.01
+    used = A.int8_k_scale_per_head(ks, b, hkv)
+    assert torch.equal(used, ks.reshape(-1)[: b * hkv].view(b, hkv))
+    out = A.decode_int8(q, k, v, qs, ks, 8, F64)
+    close(out, t64(Bt.decode_int8(q, k.float(), v.double(), qs, ks, 8)), tol=1e-6)
+
+
+# ---------------------------------------------------------------- closed forms
+
+def test_decode_cache_len_zero_returns_first_value_row():
+    g = torch.Generator().manual_seed(6)
+    q, k, v = randn(g, 2, 4, 1, 16), randn(g, 2, 2, 9, 16), randn(g, 2, 2, 9, 16)
+    out = A.decode(q, k, v, True, 0, F64)
+    close(out, A.expand_kv(v, 4)[:, :, :1].double())
+
+
+def test_identical_keys_give_mean_value():
+    g = torch.Generator().manual_seed(7)
+    q, v = randn(g, 1, 2, 6, 8), randn(g, 1, 2, 6, 8)
+    k = randn(g, 1, 2, 1, 8).expand(1, 2, 6, 8).contiguous()
+    out = A.prefill(q, k, v, False, F64)
+    close(out, v.double().mean(2, keepdim=True).expand_as(out))
+    out_c = A.prefill(q, k, v, True, F64)  # causal: running means
+    close(out_c, v.double().cumsum(2) / torch.arange(1, 7, dtype=F64).view(1, 1, 6, 1))
+
+
+def test_dominant_key_selects_its_value_row():
+    d = 16
+    q = torch.zeros(1, 1, 1, d, dtype=torch.float16)
+    q[..., 0] = 8.0
+    k = torch.zeros(1, 1, 10, d, dtype=torch.float16)
+    k[0, 0, 6, 0] = 8.0  # score 64/4 = 16 vs 0 elsewhere
+    v = torch.arange(10 * d, dtype=torch.float32).view(1, 1, 10, d).half() / 100
+    out = A.decode(q, k, v, False, 9, F64)
+    w = torch.exp(torch.tensor(16.0, dtype=F64))
+    expect = (w * v[0, 0, 6].double() + v[0, 0].double().sum(0) - v[0, 0, 6].double()) / (w + 9)
+    close(out[0, 0, 0], expect)
+
+
+def test_prefill_causal_first_row_is_first_value():
+    g = torch.Generator().manual_seed(8)
+    q, k, v = randn(g, 1, 3, 5, 8), randn(g, 1, 3, 5, 8), randn(g, 1, 3, 5, 8)
+    close(A.prefill(q, k, v, True, F64)[:, :, 0], v[:, :, 0].double())
+
+
+def test_int8_exact_codes_reduce_to_float_decode():
+    """With q = qi*q_s and k = ki*k_s exactly representable, quantization is
+    lossless and the INT8 path must equal plain decode (no dropped term/scale)."""
+    g = torch.Generator().manual_seed(10)
+    b, hq, hkv, n, d = 2, 4, 2, 7, 16
+    qi = torch.randint(-127, 128, (b, hq, 1, d), generator=g).float()
+    ki = torch.randint(-127, 128, (b, hkv, n, d), generator=g).float()
+    qs = torch.full((b, hq), 2.0 ** -7)
+    ks = torch.full((b, hkv, n), 2.0 ** -6)
+    q, k = (qi * 2.0 ** -7).half(), (ki * 2.0 ** -6).half()
+    v = randn(g, b, hkv, n, d)
+    out = A.decode_int8(q, k, v, qs, ks, 5, F64)
+    ref = A.decode(q, k, v, True, 5, F64)
+    close(out, ref, tol=1e-5)
+
+
+def test_roundf_ties_away_from_zero():
+    s = torch.tensor([1.0])
+    x = torch.tensor([2.5, -2.5, 0.5, -0.5, 1.4990234375, 126.5, 300.0, -300.0]).half()  # all exact in fp16
+    got = A.quantize_int8(x, s).tolist()
+    assert got == [3, -3, 1, -1, 1, 127, 127, -127]
+
+
+def test_gqa_equals_expanded_mha():
+    g = torch.Generator().manual_seed(11)
+    q, k, v = randn(g, 2, 8, 12, 8), randn(g, 2, 2, 12, 8), randn(g, 2, 2, 12, 8)
+    close(A.prefill(q, k, v, True, F64),
+          A.prefill(q, k.repeat_interleave(4, 1), v.repeat_interleave(4, 1), True, F64))
+    # head h uses kv head h // 4 (not h % 2)
+    alt = A.prefill(q, k.repeat(1, 4, 1, 1), v.repeat(1, 4, 1, 1), True, F64)
+    assert not torch.allclose(alt, A.prefill(q, k, v, True, F64))
+
+
+def test_continuous_batching_equals_per_row_decode():
+    g = torch.Generator().manual_seed(12)
+    q, k, v = randn(g, 3, 4, 1, 8), randn(g, 3, 2, 20, 8), randn(g, 3, 2, 20, 8)
+    cl = torch.tensor([0, 7, 30], dtype=torch.int32)
+    out = A.continuous_batching(q, k, v, cl, True, F64)
+    for i, c in enumerate(cl.tolist()):
+        n = min(c + 1, 20)
+        close(out[i:i + 1], A.decode(q[i:i + 1], k[i:i + 1, :, :n], v[i:i + 1, :, :n], True, n - 1, F64))
+
+
+# ---------------------------------------------------------------- golden fixtures
+
+def _golden_files():
+    return sorted(f for f in os.listdir(GOLDEN) if f.endswith(".pt")) if os.path.isdir(GOLDEN) else []
+
+
+def test_golden_fixtures_present():
+    assert len(_golden_files()) >= 6
+
+
+@pytest.mark.parametrize("fname", _golden_files())
+def test_oracle_matches_golden(fname):
+    fx = torch.load(os.path.join(GOLDEN, fname), weights_only=True)
+    kind = fx["kind"]
+    a = fx["args"]
+    if kind == "prefill":
+        out = A.prefill(a["q"], a["k"], a["v"], bool(a["causal"]), F64)
+    elif kind == "decode":
+        out = A.decode(a["q"], a["k"], a["v"], bool(a["causal"]), int(a["cache_len"]), F64)
+    elif kind == "continuous_batching":
+        out = A.continuous_batching(a["q"], a["k"], a["v"], a["cache_lens"], bool(a["causal"]), F64)
+    elif kind == "paged":
+        out = A.paged_decode(a["q"], a["k_cache"], a["v_cache"], a["block_table"], a["seq_lens"],
+                             int(a["max_num_blocks"]), F64)
+    elif kind == "varlen":
+        out = A.varlen_prefill(a["q"], a["k"], a["v"], a["cu_seqlens"], int(a["max_seqlen"]),
+                               bool(a["causal"]), F64)
+    elif kind == "int8":
+        out = A.decode_int8(a["q"], a["k"], a["v"], a["q_scale"], a["k_scale"], int(a["cache_len"]), F64)
+    else:
+        raise AssertionError(kind)
+    close(out, fx["out"], tol=1e-6)
