@@ -1,0 +1,340 @@
+"""Benchmark of the MI355X attention hot path on the BASELINE configs.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b] [--no-cpu]
+
+Prints ONE JSON line.  The headline ``value`` is BASELINE configs[1]: GQA decode
+via forward_decode_gqa_fp16, Q [1,32,1,128], K/V [1,8,4097,128] fp16,
+cache_len 4096, causal -- reported as algorithmic HBM GB/s (K and V rows the
+attention must read, plus Q and O), with inputs resident in HBM.  Its 16.8 MB
+working set fits in the 256 MB Infinity Cache, so every step uses the next of
+40 distinct K/V buffer sets (672 MB) and the timed loop cannot be served from
+cache.  A "step" is one call of the hot path over one batch.
+
+The line also carries, per config, the GPU time, throughput, roofline fraction
+and tokens/s (decode) or TFLOP/s (prefill), the ``roofline`` object for the
+headline kernel (timed with HIP events on the stream the kernel runs on), and
+``cpu_baseline``: the CPU oracle (PyTorch eager fp32 math attention with the
+reference's masking, oracle/attention.py) timed on this host on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+MFMA_FP16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA
+HEADLINE_KERNEL = "decode_splitkv_kernel<128, 4, 0, true>"
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--configs", default="1,2,3,4,5a,5b")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
+    return ap.parse_args()
+
+
+def time_gpu(fn, steps, warmup):
+    """Average ms per call of fn(i), timed with HIP events on the current stream."""
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    for i in range(steps):
+        fn(warmup + i)
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def time_cpu(fn, budget_s, min_reps=1):
+    """Median seconds per call of fn(), repeating until ~budget_s is spent."""
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 50:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+# ----------------------------------------------------------------------------- configs
+
+def cfg1_prefill(fa, torch, steps, warmup):
+    B, H, N, D = 2, 8, 256, 64
+    g = torch.Generator().manual_seed(0)
+    q, k, v = [torch.randn(B, H, N, D, generator=g).half() for _ in range(3)]
+    qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
+    ms = time_gpu(lambda i: fa.forward_fp16(qc, kc, vc, True), steps, warmup)
+    flops = 4.0 * B * H * D * N * (N + 1) / 2
+    tfs = flops / (ms * 1e-3) / 1e12
+    return dict(workload="forward_fp16 causal B=2 H=8 N=256 D=64", ms=ms, tflops=tfs,
+                roofline_frac=tfs / MFMA_FP16_PEAK_TFS, flops=flops,
+                ref_flops_2BHN2D=2.0 * B * H * N * N * D), (q, k, v)
+
+
+def cfg2_decode(fa, torch, steps, warmup, nsets=40):
+    B, HQ, HKV, N, D, CL = 1, 32, 8, 4097, 128, 4096
+    g = torch.Generator(device="cuda").manual_seed(0)
+    qs = [torch.randn(B, HQ, 1, D, generator=g, device="cuda").half() for _ in range(nsets)]
+    ks = [torch.randn(B, HKV, N, D, generator=g, device="cuda").half() for _ in range(nsets)]
+    vs = [torch.randn(B, HKV, N, D, generator=g, device="cuda").half() for _ in range(nsets)]
+
+    def step(i):
+        j = i % nsets
+        fa.forward_decode_gqa_fp16(qs[j], ks[j], vs[j], True, CL)
+
+    ms = time_gpu(step, steps, warmup)
+    kv_bytes = 2.0 * B * HKV * (CL + 1) * D * 2
+    total = kv_bytes + 2.0 * B * HQ * D * 2
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="forward_decode_gqa_fp16 B=1 Hq=32 Hkv=8 N=4097 D=128 cache_len=4096 causal",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total, tokens_per_s=B / (ms * 1e-3),
+                rotating_sets=nsets), (qs[0].cpu(), ks[0].cpu(), vs[0].cpu(), CL)
+
+
+def cfg3_cb(fa, torch, steps, warmup):
+    B, HQ, HKV, MAXN, D = 64, 32, 8, 8193, 128
+    g = torch.Generator().manual_seed(3)
+    cl = torch.randint(16, 8193, (B,), generator=g, dtype=torch.int32)
+    gg = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn(B, HQ, 1, D, generator=gg, device="cuda").half()
+    k = torch.randn(B, HKV, MAXN, D, generator=gg, device="cuda").half()
+    v = torch.randn(B, HKV, MAXN, D, generator=gg, device="cuda").half()
+    clc = cl.cuda()
+    ms = time_gpu(lambda i: fa.forward_continuous_batching_fp16(q, k, v, clc, True), steps, warmup)
+    rows = torch.clamp(cl.long() + 1, max=MAXN).sum().item()
+    total = rows * HKV * D * 2 * 2 + 2.0 * B * HQ * D * 2 + 4 * B
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="forward_continuous_batching_fp16 B=64 Hq=32 Hkv=8 max_N=8193 D=128 cache_lens~U[16,8192]",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total,
+                tokens_per_s=B / (ms * 1e-3)), (q, k, v, cl)
+
+
+def cfg4_paged(fa, torch, steps, warmup):
+    B, HQ, HKV, D, P, MNB = 128, 32, 8, 128, 65536, 256
+    g = torch.Generator().manual_seed(4)
+    sl = torch.randint(64, 4097, (B,), generator=g, dtype=torch.int32)
+    bt = torch.randperm(P, generator=g)[: B * MNB].view(B, MNB).int()
+    gg = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn(B, HQ, 1, D, generator=gg, device="cuda").half()
+    kc = torch.randn(P, HKV, 16, D, generator=gg, device="cuda").half()
+    vc = torch.randn(P, HKV, 16, D, generator=gg, device="cuda").half()
+    btc, slc = bt.cuda(), sl.cuda()
+    ms = time_gpu(lambda i: fa.forward_paged_decode_gqa_fp16(q, kc, vc, btc, slc, MNB), steps, warmup)
+    tok = sl.long().sum().item()
+    pages = ((sl.long() + 15) // 16).sum().item()
+    total = tok * HKV * D * 2 * 2 + pages * 4 + 2.0 * B * HQ * D * 2 + 4 * B
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="forward_paged_decode_gqa_fp16 B=128 Hq=32 Hkv=8 D=128 pages=65536x16 seq_lens~U[64,4096]",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total,
+                tokens_per_s=B / (ms * 1e-3)), (q, kc, vc, bt, sl, MNB)
+
+
+def cfg5a_varlen(fa, torch, steps, warmup):
+    H, D = 32, 128
+    g = torch.Generator().manual_seed(5)
+    lens = torch.randint(128, 2049, (16,), generator=g).tolist()
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32)
+    tot = int(cu[-1])
+    gg = torch.Generator(device="cuda").manual_seed(5)
+    q, k, v = [torch.randn(tot, H, D, generator=gg, device="cuda").half() for _ in range(3)]
+    cuc = cu.cuda()
+    ms = time_gpu(lambda i: fa.forward_varlen_prefill_fp16(q, k, v, cuc, max(lens), True), steps, warmup)
+    flops = sum(4.0 * H * D * L * (L + 1) / 2 for L in lens)
+    tfs = flops / (ms * 1e-3) / 1e12
+    return dict(workload="forward_varlen_prefill_fp16 16 seqs L~U[128,2048] H=32 D=128 causal",
+                ms=ms, tflops=tfs, roofline_frac=tfs / MFMA_FP16_PEAK_TFS, flops=flops, total_tokens=tot,
+                tokens_per_s=tot / (ms * 1e-3)), (q, k, v, cu, lens)
+
+
+def cfg5b_int8(fa, torch, steps, warmup, nsets=5):
+    B, HQ, HKV, N, D, CL = 16, 32, 8, 2049, 128, 2048
+    gg = torch.Generator(device="cuda").manual_seed(55)
+    sets = []
+    for _ in range(nsets):
+        q = torch.randn(B, HQ, 1, D, generator=gg, device="cuda").half()
+        k = torch.randn(B, HKV, N, D, generator=gg, device="cuda").half()
+        v = torch.randn(B, HKV, N, D, generator=gg, device="cuda").half()
+        qs = (q.float().abs().amax(-1).squeeze(-1) / 127).contiguous()
+        ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(B, HKV, N).contiguous()
+        sets.append((q, k, v, qs, ks))
+
+    def step(i):
+        q, k, v, qs, ks = sets[i % nsets]
+        fa.forward_decode_int8_gqa(q, k, v, qs, ks, CL)
+
+    ms = time_gpu(step, steps, warmup)
+    total = 2.0 * B * HKV * (CL + 1) * D * 2 + 2.0 * B * HQ * D * 2 + 4.0 * B * HQ + 4.0 * B * HKV
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="forward_decode_int8_gqa B=16 Hq=32 Hkv=8 N=2049 D=128 cache_len=2048",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total, tokens_per_s=B / (ms * 1e-3),
+                rotating_sets=nsets), sets[0]
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+def cpu_baseline_cfg2(torch, sample, budget_s=12.0):
+    """Oracle decode on the full config-2 problem (it is small), repeated for ~budget_s."""
+    from oracle import attention as A
+
+    q, k, v, cl = sample
+    sec, reps = time_cpu(lambda: A.decode(q, k, v, True, cl), budget_s, min_reps=3)
+    kv_bytes = 2.0 * k.shape[0] * k.shape[1] * (cl + 1) * k.shape[3] * 2 + 2.0 * q.numel() * 2
+    return dict(value=kv_bytes / sec / 1e9, unit="GB/s", ms=sec * 1e3, reps=reps,
+                sample="full config 2 (B=1, 32:8 heads, 4097 keys, D=128), median of %d runs" % reps)
+
+
+def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
+    """Oracle on bounded samples of the other configs (a few sequences each)."""
+    from oracle import attention as A
+
+    out = {}
+    if "1" in samples:
+        q, k, v = samples["1"]
+        sec, n = time_cpu(lambda: A.prefill(q, k, v, True), budget_s, min_reps=3)
+        f = results["1"]["flops"]
+        out["1"] = dict(ms=sec * 1e3, tflops=f / sec / 1e12, sample="full config 1")
+    if "3" in samples:
+        q, k, v, cl = samples["3"]
+        idx = list(range(4))
+        qs, ks, vs = q[idx].cpu(), k[idx].cpu(), v[idx].cpu()
+        sec, n = time_cpu(lambda: A.continuous_batching(qs, ks, vs, cl[idx], True), budget_s)
+        rows = torch.clamp(cl[idx].long() + 1, max=k.shape[2]).sum().item()
+        by = rows * k.shape[1] * k.shape[3] * 4
+        out["3"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
+                        sample="4 of 64 sequences")
+    if "4" in samples:
+        q, kc, vc, bt, sl, mnb = samples["4"]
+        idx = list(range(4))
+        pages = torch.unique(bt[idx].reshape(-1)).long()
+        # gather only the pages the 4 sequences use, remapping the table
+        remap = torch.full((kc.shape[0],), -1, dtype=torch.int32)
+        remap[pages] = torch.arange(pages.numel(), dtype=torch.int32)
+        kcs, vcs = kc[pages.cuda()].cpu(), vc[pages.cuda()].cpu()
+        bts = remap[bt[idx].long()]
+        qs = q[idx].cpu()
+        sec, n = time_cpu(lambda: A.paged_decode(qs, kcs, vcs, bts, sl[idx], mnb), budget_s)
+        by = sl[idx].long().sum().item() * kc.shape[1] * kc.shape[3] * 4
+        out["4"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
+                        sample="4 of 128 sequences")
+    if "5a" in samples:
+        q, k, v, cu, lens = samples["5a"]
+        s, n_ = int(cu[0]), lens[0]
+        qs, ks, vs = q[s:s + n_, :4].cpu(), k[s:s + n_, :4].cpu(), v[s:s + n_, :4].cpu()
+        cu1 = torch.tensor([0, n_], dtype=torch.int32)
+        sec, _ = time_cpu(lambda: A.varlen_prefill(qs, ks, vs, cu1, n_, True), budget_s)
+        f = 4.0 * 4 * 128 * n_ * (n_ + 1) / 2
+        out["5a"] = dict(ms=sec * 1e3, tflops=f / sec / 1e12, sample=f"1 sequence (L={n_}), 4 of 32 heads")
+    if "5b" in samples:
+        q, k, v, qs_, ks_ = samples["5b"]
+        idx = [0, 1]
+        args = [t[idx].cpu() for t in (q, k, v, qs_, ks_)]
+        cl = k.shape[2] - 1
+        sec, _ = time_cpu(lambda: A.decode_int8(*args, cl), budget_s)
+        by = 2.0 * len(idx) * k.shape[1] * (cl + 1) * k.shape[3] * 2
+        out["5b"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
+                         sample="2 of 16 sequences")
+    return out
+
+
+# ----------------------------------------------------------------------------- main
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note "
+                                   "(DESIGN.md), not a measured path", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+
+    import flash_attn_v100 as fa
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    torch.backends.cuda.matmul.allow_tf32 = False
+    want = [c.strip() for c in args.configs.split(",") if c.strip()]
+    if args.only_headline:
+        want = ["2"]
+    results, samples = {}, {}
+    runners = {
+        "1": lambda: cfg1_prefill(fa, torch, 500, 50),
+        "2": lambda: cfg2_decode(fa, torch, args.steps, args.warmup),
+        "3": lambda: cfg3_cb(fa, torch, 30, 5),
+        "4": lambda: cfg4_paged(fa, torch, 30, 5),
+        "5a": lambda: cfg5a_varlen(fa, torch, 20, 3),
+        "5b": lambda: cfg5b_int8(fa, torch, 100, 10),
+    }
+    for c in ["1", "2", "3", "4", "5a", "5b"]:
+        if c not in want:
+            continue
+        log(f"config {c} ...")
+        r, s = runners[c]()
+        results[c], samples[c] = r, s
+        log(f"config {c}: " + json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}))
+        if c in ("3", "4"):
+            del s  # keep only what the CPU leg needs
+        torch.cuda.empty_cache()
+
+    cpu = None
+    cores = torch.get_num_threads()
+    if not args.no_cpu and "2" in results:
+        log(f"CPU baseline on {cores} threads (os.cpu_count()={os.cpu_count()}) ...")
+        cpu2 = cpu_baseline_cfg2(torch, samples["2"])
+        cpu_other = cpu_baseline_sampled(torch, results, {k: v for k, v in samples.items() if k != "2"})
+        cpu = dict(value=cpu2["value"], unit="GB/s", cores=cores, kind="port", sample=cpu2["sample"],
+                   ms=cpu2["ms"], other_configs=cpu_other, os_cpu_count=os.cpu_count())
+        for c, r in cpu_other.items():
+            results[c]["cpu"] = r
+
+    head = results["2"]
+    line = {
+        "metric": "decode GQA attn HBM GB/s (% of peak); prefill fp16 TFLOP/s (% MFMA peak)",
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1) fp16, seeded; K/V rotated over 40 buffer sets (672 MB) to defeat the 256 MB MALL",
+        "config": {"workload": head["workload"], "baseline_config": "configs[1]", "global_batch": 1,
+                   "seq_len": 4097, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": HEADLINE_KERNEL, "avg_launch_us": round(head["ms"] * 1e3, 3),
+                     "timing": "HIP events on the launch stream around %d back-to-back calls" % args.steps},
+        "cpu_baseline": cpu,
+        "configs": {c: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()}
+                    for c, r in results.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

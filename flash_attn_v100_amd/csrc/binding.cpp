@@ -14,6 +14,7 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <cmath>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/flash_attn_mi355x.h"
@@ -143,11 +144,39 @@ void check_prefill_gqa_output_tensor(const at::Tensor& out, const at::Tensor& q)
   TORCH_CHECK(out.sizes() == q.sizes(), "out shape must match q shape for prefill mode");
 }
 
-// Split-KV partials live in a torch-allocated scratch tensor on the launch stream.
+// Split-KV workspace: one zero-filled buffer per (device, stream), grown on
+// demand and kept for the life of the process.  The kernels leave its arrival
+// counters at zero after every call, and calls on one stream run in order, so
+// the buffer never needs clearing again.  Distinct streams get distinct buffers,
+// so concurrent calls never share counters.  (The GIL serialises this map.)
+struct WorkspaceKey {
+  int device;
+  uintptr_t stream;
+  bool operator==(const WorkspaceKey& o) const { return device == o.device && stream == o.stream; }
+};
+struct WorkspaceKeyHash {
+  size_t operator()(const WorkspaceKey& k) const { return std::hash<uintptr_t>()(k.stream) ^ (size_t)k.device; }
+};
+
 at::Tensor decode_workspace(const at::Tensor& q, int B, int H_Q, int H_KV, int max_len, int D) {
+  // Deliberately leaked: destroying tensors after the HIP runtime shut down at exit is unsafe.
+  static auto& cache = *new std::unordered_map<WorkspaceKey, at::Tensor, WorkspaceKeyHash>();
   const size_t bytes = fa_decode_workspace_size(B, H_Q, H_KV, max_len, D);
-  return at::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, q.options().dtype(at::kByte));
+  if (bytes == 0) return at::Tensor();
+  const WorkspaceKey key{q.device().index(), reinterpret_cast<uintptr_t>(cur_stream())};
+  auto it = cache.find(key);
+  if (it != cache.end() && static_cast<size_t>(it->second.numel()) >= bytes) return it->second;
+  // Grow geometrically; the old buffer returns to the caching allocator, which
+  // reuses it only for work ordered after the calls already queued on this stream.
+  size_t alloc = bytes;
+  if (it != cache.end()) alloc = std::max(bytes, static_cast<size_t>(it->second.numel()) * 2);
+  at::Tensor ws = at::zeros({static_cast<int64_t>(alloc)}, q.options().dtype(at::kByte));
+  cache[key] = ws;
+  return ws;
 }
+
+void* ws_ptr(const at::Tensor& ws) { return ws.defined() ? ws.data_ptr() : nullptr; }
+size_t ws_bytes(const at::Tensor& ws) { return ws.defined() ? static_cast<size_t>(ws.numel()) : 0; }
 
 // ---------------------------------------------------------------------------
 // Prefill
@@ -252,7 +281,7 @@ void launch_decode(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v
   const int N = to_int(k.size(2), "N"), D = to_int(q.size(3), "D");
   auto ws = decode_workspace(q, B, H_Q, H_KV, N, D);
   check_fa(fa_decode_fp16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H_Q, H_KV, N, D,
-                          causal ? 1 : 0, cache_len, ws.data_ptr(), static_cast<size_t>(ws.numel()),
+                          causal ? 1 : 0, cache_len, ws_ptr(ws), ws_bytes(ws),
                           cur_stream()));
 }
 
@@ -348,7 +377,7 @@ at::Tensor forward_continuous_batching_fp16(at::Tensor q, at::Tensor k, at::Tens
   auto ws = decode_workspace(q, B, hq, hkv, max_N, d);
   check_fa(fa_continuous_batching_fp16(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                        cache_lens.data_ptr<int32_t>(), B, hq, hkv, max_N, d, causal ? 1 : 0,
-                                       ws.data_ptr(), static_cast<size_t>(ws.numel()), cur_stream()));
+                                       ws_ptr(ws), ws_bytes(ws), cur_stream()));
   return out;
 }
 
@@ -394,8 +423,7 @@ at::Tensor forward_paged_decode_gqa_fp16(at::Tensor q, at::Tensor k_cache, at::T
   check_fa(fa_paged_decode_gqa_fp16(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), out.data_ptr(),
                                     block_table.data_ptr<int32_t>(), block_table.numel(),
                                     seq_lens.data_ptr<int32_t>(), b, hq, hkv, d,
-                                    to_int(k_cache.size(0), "num_pages"), max_num_blocks, ws.data_ptr(),
-                                    static_cast<size_t>(ws.numel()), cur_stream()));
+                                    to_int(k_cache.size(0), "num_pages"), max_num_blocks, ws_ptr(ws), ws_bytes(ws), cur_stream()));
   return out;
 }
 
@@ -429,7 +457,7 @@ at::Tensor forward_decode_int8_gqa(at::Tensor q, at::Tensor k, at::Tensor v, at:
   auto ws = decode_workspace(q, b, hq, hkv, n, d);
   check_fa(fa_decode_int8_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                               q_scale.data_ptr<float>(), k_scale.data_ptr<float>(), b, hq, hkv, n, d, cache_len,
-                              ws.data_ptr(), static_cast<size_t>(ws.numel()), cur_stream()));
+                              ws_ptr(ws), ws_bytes(ws), cur_stream()));
   return out;
 }
 

@@ -74,6 +74,24 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
+// Device-coherent scalar store / load: relaxed atomics at agent scope, which
+// gfx950 issues as sc1 global stores/loads that bypass the (per-XCD, not
+// mutually coherent) L2 caches.  Used for data handed between workgroups.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// s_waitcnt vmcnt(0): this thread's vector memory operations, stores included,
+// have completed.  (GFX9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15.)
+__device__ __forceinline__ void wait_vmem_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Eight fp16 values starting at column `col` of a row of length `d`.  VEC: the
 // row base is 16-byte aligned and d % 8 == 0, so one dwordx4 load serves.
 template <bool VEC>

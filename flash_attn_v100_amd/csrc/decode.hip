@@ -14,9 +14,13 @@
 // over the lane's 8 columns followed by a DPP reduction over the LPR lanes of
 // the row; each group of LPR lanes keeps its own online-softmax state
 // (m, l, acc[8]) for the rows it owns, and the states are merged across lanes
-// and waves only once, at the end of the split.  Splits either write the fp16
-// output directly (one split) or a (log2-sum-exp, normalised output) partial
-// that decode_combine_kernel merges.
+// and waves only once, at the end of the split.  A sequence covered by one
+// split writes the fp16 output directly; otherwise each split writes a
+// (log2-sum-exp, normalised output) partial, bumps its unit's arrival counter,
+// and the last split to arrive merges the partials -- one kernel per call, no
+// separate combine launch.  The last split also resets the counter, so a
+// zero-filled workspace stays zero-filled between calls (and across graph
+// replays) without any memset.
 #include <math.h>
 
 #include "capi_internal.h"
@@ -45,6 +49,8 @@ struct DecodeParams {
   const float* k_scale;        // INT8
   float* ws_o;                 // [B*H_Q, S, DP] normalised partial outputs
   float* ws_lse;               // [B*H_Q, S] log2-sum-exp of each partial
+  unsigned* counters;          // [kCounterSlots] arrivals per unit of a launch; zero between calls
+  int unit_base;               // first unit of this launch
   int B, H_Q, H_KV, N, D, G;
   int fixed_len;               // decode / INT8: number of attended keys
   int chunk, num_splits, num_hg;
@@ -90,7 +96,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 
   const int S = p.num_splits;
   const int split = blockIdx.x % S;
-  const int rest = blockIdx.x / S;
+  const int slot = blockIdx.x / S;      // this launch's counter slot
+  const int rest = p.unit_base + slot;  // (b, h_kv, head group) unit
   const int hg = rest % p.num_hg;
   const int pair = rest / p.num_hg;
   const int b = pair / p.H_KV;
@@ -110,9 +117,9 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   const int k1 = min(L, k0 + p.chunk);
 
   if (k0 >= k1) {
-    // Empty range.  With a single split nobody else writes this output: the
-    // reference's acc/l_i is 0/0 there.
-    if (S == 1 && split == 0) {
+    // No key at all (L <= 0): the reference's acc/l_i is 0/0 there.  Split 0
+    // writes the NaN; other empty splits just leave.
+    if (L <= 0 && split == 0) {
       for (int i = tid; i < GB * D; i += kDecThreads) {
         const int g = i / D, d = i % D;
         if (g_base + g < G) {
@@ -124,10 +131,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     return;
   }
 
-  __shared__ int s_pages[kMaxChunk / kPage];
+  __shared__ int s_pages[MODE == kModePaged ? kMaxChunk / kPage : 1];
   __shared__ int s_bad;
   if constexpr (MODE == kModePaged) {
-    if (tid == 0) s_bad = 0;
+    // A sequence longer than its table row would read the next row's page ids.
+    if (tid == 0) s_bad = static_cast<long long>(L) > static_cast<long long>(p.max_num_blocks) * kPage;
     __syncthreads();
     const int np = (k1 - k0 + kPage - 1) / kPage;
     for (int i = tid; i < np; i += kDecThreads) {
@@ -299,6 +307,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 
   bool bad = false;
   if constexpr (MODE == kModePaged) bad = s_bad != 0;
+  // Splits that hold keys of this sequence (>= 1 here, since k0 < k1).
+  const int sb = min(S, (L + p.chunk - 1) / p.chunk);
 
   for (int i = tid; i < GB * DP; i += kDecThreads) {
     const int g = i / DP, d = i % DP;
@@ -318,38 +328,50 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     if (bad) outv = lse = __builtin_nanf("");
     const int h = hkv * G + g_base + g;
     const size_t bh = static_cast<size_t>(b) * p.H_Q + h;
-    if (S == 1) {
+    if (sb == 1) {
       p.o[bh * D + d] = static_cast<half_t>(outv);
     } else {
       const size_t e = bh * S + split;
-      p.ws_o[e * DP + d] = outv;
-      if (d == 0) p.ws_lse[e] = lse;
+      store_coherent(&p.ws_o[e * DP + d], outv);
+      if (d == 0) store_coherent(&p.ws_lse[e], lse);
     }
   }
-}
+  if (sb == 1) return;
 
-// Merges the per-split partials of one (b, h_q) into the fp16 output.
-template <int DP, int MODE>
-__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeParams p) {
-  const int bh = blockIdx.x;
-  const int b = bh / p.H_Q;
-  const int S = p.num_splits;
-  const int L = seq_len_of<MODE>(p, b);
-  const int sb = L <= 0 ? 0 : min(S, (L + p.chunk - 1) / p.chunk);
-  const float* lse = p.ws_lse + static_cast<size_t>(bh) * S;
-  const float* po = p.ws_o + static_cast<size_t>(bh) * S * DP;
-  float mx = -INFINITY;
-  for (int s = 0; s < sb; ++s) mx = fmaxf(mx, lse[s]);
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    float num = 0.0f, den = 0.0f;
-    for (int s = 0; s < sb; ++s) {
-      const float w = fast_exp2(lse[s] - mx);
-      den += w;
-      num += w * po[static_cast<size_t>(s) * DP + d];
-    }
-    // sb == 0: 0/0 = NaN, the reference's result for an empty key range.
-    p.o[static_cast<size_t>(bh) * p.D + d] = static_cast<half_t>(sb == 0 ? __builtin_nanf("") : num / den);
+  // ---- the last split of this (b, h_kv, head group) to finish merges all partials ----
+  // Partials travel through device-coherent (L2-bypassing, sc1) stores and loads,
+  // so no whole-L2 writeback/invalidate fence is needed: each thread waits for its
+  // stores to complete, the barrier orders that before thread 0's counter atomic,
+  // and the last arrival reads the partials with coherent loads.
+  __shared__ int s_last;
+  wait_vmem_stores();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = atomicAdd(&p.counters[slot], 1u);
+    s_last = (prev == static_cast<unsigned>(sb - 1));
   }
+  __syncthreads();
+  if (!s_last) return;
+
+  for (int i = tid; i < GB * DP; i += kDecThreads) {
+    const int g = i / DP, d = i % DP;
+    if (g_base + g >= G || d >= D) continue;
+    const int h = hkv * G + g_base + g;
+    const size_t bh = static_cast<size_t>(b) * p.H_Q + h;
+    const float* lse = p.ws_lse + bh * S;
+    const float* po = p.ws_o + bh * S * DP;
+    float mx = -INFINITY;
+    for (int sp = 0; sp < sb; ++sp) mx = fmaxf(mx, load_coherent(&lse[sp]));
+    float num = 0.0f, den = 0.0f;
+    for (int sp = 0; sp < sb; ++sp) {
+      const float w = fast_exp2(load_coherent(&lse[sp]) - mx);
+      den += w;
+      num += w * load_coherent(&po[static_cast<size_t>(sp) * DP + d]);
+    }
+    p.o[bh * D + d] = static_cast<half_t>(num / den);
+  }
+  // Leave the counter at zero for the next call on this workspace.
+  if (tid == 0) atomicExch(&p.counters[slot], 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -378,11 +400,30 @@ static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D) {
   return pl;
 }
 
-static size_t plan_workspace(const DecodePlan& pl, int B, int H_Q) {
-  if (pl.splits <= 1) return 0;
+static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+// Workspace layout: [counters: kCounterSlots x u32][lse: B*H_Q*S f32][partials: B*H_Q*S*DP f32],
+// each region 256-byte aligned.  Needed only when a sequence can span several
+// splits.  The counter region has the same size and place for every call, so
+// one workspace can serve calls of any shape: no call's partials ever land on
+// another call's counters.  A launch covers at most kCounterSlots units; larger
+// problems are issued as several launches over unit ranges.
+constexpr size_t kCounterSlots = 65536;
+
+struct WorkspaceLayout {
+  size_t counters, lse, o, total;
+};
+
+static WorkspaceLayout plan_layout(const DecodePlan& pl, int B, int H_Q, int H_KV) {
+  (void)H_KV;
+  WorkspaceLayout w = {0, 0, 0, 0};
+  if (pl.splits <= 1) return w;
   const size_t entries = static_cast<size_t>(B) * H_Q * pl.splits;
-  const size_t lse = (entries * sizeof(float) + 255) & ~static_cast<size_t>(255);
-  return lse + entries * pl.dp * sizeof(float);
+  w.counters = 0;
+  w.lse = align256(kCounterSlots * sizeof(unsigned));
+  w.o = w.lse + align256(entries * sizeof(float));
+  w.total = w.o + entries * pl.dp * sizeof(float);
+  return w;
 }
 
 template <int DP, int GB, int MODE, bool VEC>
@@ -413,15 +454,6 @@ static void dispatch(const DecodePlan& pl, bool vec, const DecodeParams& p, int 
   }
 }
 
-template <int MODE>
-static void launch_combine(const DecodePlan& pl, const DecodeParams& p, hipStream_t st) {
-  const int blocks = p.B * p.H_Q;
-  const int threads = pl.dp;
-  if (pl.dp == 64) hipLaunchKernelGGL((decode_combine_kernel<64, MODE>), dim3(blocks), dim3(threads), 0, st, p);
-  else if (pl.dp == 128) hipLaunchKernelGGL((decode_combine_kernel<128, MODE>), dim3(blocks), dim3(threads), 0, st, p);
-  else hipLaunchKernelGGL((decode_combine_kernel<256, MODE>), dim3(blocks), dim3(threads), 0, st, p);
-}
-
 static int check_common(const char* fn, int B, int H_Q, int H_KV, int D) {
   if (B < 0 || H_Q <= 0 || H_KV <= 0 || D <= 0)
     return set_error(FA_ERR_INVALID_ARG, "%s: sizes must be positive (B=%d H_Q=%d H_KV=%d D=%d)", fn, B, H_Q, H_KV, D);
@@ -434,7 +466,8 @@ static int check_common(const char* fn, int B, int H_Q, int H_KV, int D) {
 template <int MODE>
 static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, size_t ws_bytes, void* stream) {
   const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D);
-  const size_t need = plan_workspace(pl, p.B, p.H_Q);
+  const WorkspaceLayout wl = plan_layout(pl, p.B, p.H_Q, p.H_KV);
+  const size_t need = wl.total;
   if (need > 0 && (ws == nullptr || ws_bytes < need))
     return set_error(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", fn, need, ws_bytes);
   if (p.B == 0) return FA_OK;
@@ -445,23 +478,22 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   p.scale = 1.0f / sqrtf(static_cast<float>(p.D));
   p.scale_log2 = p.scale * kLog2e;
   if (need > 0) {
-    const size_t entries = static_cast<size_t>(p.B) * p.H_Q * pl.splits;
-    const size_t lse_bytes = (entries * sizeof(float) + 255) & ~static_cast<size_t>(255);
-    p.ws_lse = static_cast<float*>(ws);
-    p.ws_o = reinterpret_cast<float*>(static_cast<char*>(ws) + lse_bytes);
+    char* base = static_cast<char*>(ws);
+    p.counters = reinterpret_cast<unsigned*>(base + wl.counters);
+    p.ws_lse = reinterpret_cast<float*>(base + wl.lse);
+    p.ws_o = reinterpret_cast<float*>(base + wl.o);
   }
   const bool vec = (p.D % 8 == 0) && aligned16(p.q) && aligned16(p.k) && aligned16(p.v);
-  const long long blocks = static_cast<long long>(p.B) * p.H_KV * pl.num_hg * pl.splits;
-  if (blocks > 0x7fffffffLL) return set_error(FA_ERR_UNSUPPORTED, "%s: problem too large for one launch", fn);
+  const long long units = static_cast<long long>(p.B) * p.H_KV * pl.num_hg;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  dispatch<MODE>(pl, vec, p, static_cast<int>(blocks), st);
-  int rc = check_launch(fn);
-  if (rc != FA_OK) return rc;
-  if (pl.splits > 1) {
-    launch_combine<MODE>(pl, p, st);
-    rc = check_launch(fn);
+  for (long long u0 = 0; u0 < units; u0 += static_cast<long long>(kCounterSlots)) {
+    const long long nu = units - u0 < static_cast<long long>(kCounterSlots) ? units - u0 : kCounterSlots;
+    p.unit_base = static_cast<int>(u0);
+    dispatch<MODE>(pl, vec, p, static_cast<int>(nu * pl.splits), st);
+    const int rc = check_launch(fn);
+    if (rc != FA_OK) return rc;
   }
-  return rc;
+  return FA_OK;
 }
 
 }  // namespace fa
@@ -470,7 +502,7 @@ using namespace fa;
 
 extern "C" size_t fa_decode_workspace_size(int B, int H_Q, int H_KV, int max_len, int D) {
   if (B <= 0 || H_Q <= 0 || H_KV <= 0 || D <= 0 || D > 256 || H_Q % H_KV != 0) return 0;
-  return plan_workspace(make_plan(B, H_Q, H_KV, max_len, D), B, H_Q);
+  return plan_layout(make_plan(B, H_Q, H_KV, max_len, D), B, H_Q, H_KV).total;
 }
 
 extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void* o, int B, int H_Q,
@@ -540,14 +572,11 @@ extern "C" int fa_paged_decode_gqa_fp16(const void* q, const void* k_cache, cons
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = 0; p.D = D;
   p.max_num_blocks = max_num_blocks;
   p.num_pages = num_pages;
-  // Sequences longer than 16*max_num_blocks read past their own table row, as
-  // the reference does; the split plan must still cover them, so the planned
-  // length is the longest length whose table reads stay inside the table.
-  long long plan_len = max_len_ll;
-  if (block_table_numel > plan_len) plan_len = block_table_numel * kPage;
-  if (plan_len > 0x3fffffffLL) plan_len = 0x3fffffffLL;
-  if (plan_len < 1) plan_len = 1;
-  return run_decode<kModePaged>(fn, p, static_cast<int>(plan_len), workspace, workspace_bytes, stream);
+  // Splits cover tokens [0, 16*max_num_blocks); a sequence longer than its
+  // table row is reported as NaN by the last split (the reference would read
+  // the next row's page ids there).
+  const int plan_len = max_len_ll > 0 ? static_cast<int>(max_len_ll) : 1;
+  return run_decode<kModePaged>(fn, p, plan_len, workspace, workspace_bytes, stream);
 }
 
 extern "C" int fa_decode_int8_gqa(const void* q, const void* k, const void* v, void* o,

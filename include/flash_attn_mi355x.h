@@ -5,8 +5,11 @@
  * (`stream` is a hipStream_t passed as void*, NULL = the null stream).  Every
  * tensor is a dense row-major fp16 array in device memory unless stated.  The
  * library never allocates: split-KV decode entry points take a caller-owned
- * device workspace whose size comes from fa_decode_workspace_size().  All calls
- * are asynchronous on `stream`, stateless and reentrant.
+ * device workspace whose size comes from fa_decode_workspace_size().  The
+ * workspace must be zero-filled before its first use; every call leaves it
+ * zero-filled again when it completes, so one workspace serves any number of
+ * calls issued in order on one stream (calls that may overlap need separate
+ * workspaces).  All calls are asynchronous on `stream` and otherwise stateless.
  *
  * Return value: FA_OK (0) or an FA_ERR_* code; fa_last_error() gives a
  * human-readable message for the calling thread's most recent failure.
@@ -105,9 +108,11 @@ int fa_continuous_batching_fp16(const void* q, const void* k, const void* v,
  *   q/o [B, H_Q, 1, D]; k_cache/v_cache [num_pages, H_KV, 16, D];
  *   block_table int32 (device), read as flat[b * max_num_blocks + t / 16] for
  *   token t (block_table_numel bounds that read); seq_lens int32 [B] (device).
- *   Sequence b attends tokens [0, seq_lens[b]); seq_lens[b] <= 0, a page id
- *   outside [0, num_pages) or a table index past block_table_numel yields NaN
- *   for that sequence (the reference reads out of bounds there).
+ *   Sequence b attends tokens [0, seq_lens[b]).  seq_lens[b] <= 0 yields NaN
+ *   (0/0, as in the reference).  A page id outside [0, num_pages), a table
+ *   index past block_table_numel or seq_lens[b] > 16 * max_num_blocks also
+ *   yields NaN for that sequence; the reference reads out of bounds or into the
+ *   next table row there.
  * Replaces the launch in flash_attn_forward_paged_decode_gqa_fp16
  * (flash_attn_kernel.cu:3516-3584).
  */

@@ -116,12 +116,23 @@ def test_capi_decode_prefill_on_gpu(lib):
     qc, kc, vc = q.cuda(), k.cuda(), v.cuda()
     o = torch.empty_like(qc)
     ws_bytes = lib.fa_decode_workspace_size(1, 32, 8, 4097, 128)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")  # zero-filled before first use
     rc = lib.fa_decode_fp16(_p(qc), _p(kc), _p(vc), _p(o), 1, 32, 8, 4097, 128, 1, 4096, _p(ws),
                             ctypes.c_size_t(ws_bytes), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == FA_OK, lib.fa_last_error()
     torch.cuda.synchronize()
-    assert_close(o, A.decode(q, k, v, True, 4096), what="capi decode")
+    ref = A.decode(q, k, v, True, 4096)
+    assert_close(o, ref, what="capi decode")
+    # the call left the workspace's arrival counters at zero: reuse it twice more
+    for _ in range(2):
+        o2 = torch.empty_like(qc)
+        rc = lib.fa_decode_fp16(_p(qc), _p(kc), _p(vc), _p(o2), 1, 32, 8, 4097, 128, 1, 4096, _p(ws),
+                                ctypes.c_size_t(ws_bytes), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == FA_OK
+        torch.cuda.synchronize()
+        assert torch.equal(o2, o)
+    counters = ws[:256].cpu()
+    assert int(counters.sum()) == 0
     # prefill
     q, k, v = randn(g, 2, 8, 256, 64), randn(g, 2, 8, 256, 64), randn(g, 2, 8, 256, 64)
     qc, kc, vc = q.cuda(), k.cuda(), v.cuda()

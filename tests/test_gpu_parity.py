@@ -136,6 +136,55 @@ def test_decode_gqa_config2(fa):
     assert_close(out, A.decode(q, k, v, True, 4096), what="config2")
 
 
+def test_decode_split_workspace_reuse(fa):
+    """The fused split combine leaves its arrival counters at zero: repeated calls,
+    calls with other shapes in between, and calls on another stream all agree."""
+    g = gen(21)
+    q, k, v = randn(g, 2, 32, 1, 128), randn(g, 2, 8, 9000, 128), randn(g, 2, 8, 9000, 128)
+    qc, kc, vc = cuda(q, k, v)
+    ref = A.decode(q, k, v, True, 8000)
+    first = fa.forward_decode_gqa_fp16(qc, kc, vc, True, 8000)
+    assert_close(first, ref, what="split decode")
+    q2, k2, v2 = cuda(randn(g, 1, 8, 1, 64), randn(g, 1, 2, 3000, 64), randn(g, 1, 2, 3000, 64))
+    for i in range(5):
+        fa.forward_decode_gqa_fp16(q2, k2, v2, False, 0)
+        again = fa.forward_decode_gqa_fp16(qc, kc, vc, True, 8000)
+        assert torch.equal(again, first), f"iteration {i}"
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        other = fa.forward_decode_gqa_fp16(qc, kc, vc, True, 8000)
+    s.synchronize()
+    assert torch.equal(other, first)
+
+
+def test_decode_workspace_shared_across_shapes(fa):
+    """Calls of different shapes share one workspace per stream: a call with few
+    units and large partials (B=1, D=256, many splits) must not disturb the split
+    counters of a following call with many units (B=16)."""
+    g = gen(23)
+    a = [randn(g, 1, 16, 1, 256), randn(g, 1, 2, 3000, 256), randn(g, 1, 2, 3000, 256)]
+    b = [randn(g, 16, 32, 1, 128), randn(g, 16, 8, 1025, 128), randn(g, 16, 8, 1025, 128)]
+    ac, bc = cuda(*a), cuda(*b)
+    ref_b = A.decode(*b, True, 1024)
+    for _ in range(3):
+        fa.forward_decode_gqa_fp16(*ac, True, 2999)
+        assert_close(fa.forward_decode_gqa_fp16(*bc, True, 1024), ref_b, what="after small-unit call")
+        qs, ks = int8_scales(b[0], b[1])
+        out = fa.forward_decode_int8_gqa(*bc, qs.cuda(), ks.cuda(), 1024)
+        assert_close(out, A.decode_int8(*b, qs, ks, 1024), what="int8 after small-unit call")
+
+
+def test_paged_decode_sequence_longer_than_table_row_is_nan(fa):
+    g = gen(22)
+    q, kc, vc = randn(g, 2, 4, 1, 64), randn(g, 8, 2, 16, 64), randn(g, 8, 2, 16, 64)
+    bt = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32)
+    slt = torch.tensor([40, 20], dtype=torch.int32)  # 40 > 16 * max_num_blocks
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), 2)
+    assert torch.isnan(out[0].float()).all()
+    assert_close(out[1:], A.paged_decode(q[1:], kc, vc, bt[1:], slt[1:], 2), what="paged row 1")
+
+
 def test_decode_gqa_out_and_stream(fa):
     """_out writes into the caller's tensor; _stream equals the default (test_async.py:37-65)."""
     g = gen(7)
