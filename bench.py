@@ -46,6 +46,9 @@ def parse():
     ap.add_argument("--configs", default="1,2,3,4,5a,5b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="instead of benchmarking, copy an MB-sized fp16 buffer 20 times (a kernel of "
+                         "known HBM traffic, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     return ap.parse_args()
 
 
@@ -271,6 +274,16 @@ def main():
 
     import torch
 
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 2
+        src = torch.ones(n, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_copy": 2 * n, "copies": 20}))
+        return
+
     import flash_attn_v100 as fa
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -309,7 +322,15 @@ def main():
         for c, r in cpu_other.items():
             results[c]["cpu"] = r
 
+    if "2" not in results:  # partial run (e.g. under a profiler): per-config figures only
+        print(json.dumps({"configs": results}), flush=True)
+        return
     head = results["2"]
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "traffic.json")
+    if os.path.exists(tpath):  # measured by the rocprofv3 --pmc passes summarised beside it
+        with open(tpath) as f:
+            traffic = json.load(f).get(HEADLINE_KERNEL, {}).get("hbm_bytes_per_launch")
     line = {
         "metric": "decode GQA attn HBM GB/s (% of peak); prefill fp16 TFLOP/s (% MFMA peak)",
         "value": round(head["gbs"], 2),
@@ -326,7 +347,7 @@ def main():
         "config": {"workload": head["workload"], "baseline_config": "configs[1]", "global_batch": 1,
                    "seq_len": 4097, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": HEADLINE_KERNEL, "avg_launch_us": round(head["ms"] * 1e3, 3),
                      "timing": "HIP events on the launch stream around %d back-to-back calls" % args.steps},
         "cpu_baseline": cpu,

@@ -17,7 +17,7 @@
 #include <unordered_map>
 #include <vector>
 
-#include "../../include/flash_attn_mi355x.h"
+#include "flash_attn_mi355x.h"
 
 namespace {
 

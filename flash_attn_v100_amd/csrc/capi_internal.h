@@ -5,7 +5,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 
-#include "../../include/flash_attn_mi355x.h"
+#include "flash_attn_mi355x.h"
 
 namespace fa {
 

@@ -65,6 +65,17 @@ __device__ __forceinline__ int group_sum_i(int x) {
   return x;
 }
 
+// Max over the 64 lanes of a wave; every lane receives it.
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_mov<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp_mov<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp_mov<kDppRowHalfMirror>(x));
+  x = fmaxf(x, dpp_mov<kDppRowMirror>(x));
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
@@ -84,6 +95,30 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Sixteen device-coherent (sc1) loads of a float4 row slice and a float scalar
+// each -- v[j] = rows[idx[j] * row_stride .. +4), s[j] = scal[idx[j]] -- issued
+// back to back and completed by one wait, i.e. one memory round trip.  The
+// compiler offers no 16-byte coherent load (a volatile access is followed by a
+// wait after every load), so the loads are inline asm; the closing wait names
+// every destination as an operand, so no use can be scheduled before it.
+__device__ __forceinline__ void load_coherent_batch16(const float* rows, int row_stride, const float* scal,
+                                                      const int (&idx)[16], float4_t (&v)[16], float (&s)[16]) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    asm volatile("global_load_dwordx4 %0, %1, off sc1"
+                 : "=v"(v[j]) : "v"(rows + static_cast<size_t>(idx[j]) * row_stride) : "memory");
+    asm volatile("global_load_dword %0, %1, off sc1" : "=v"(s[j]) : "v"(scal + idx[j]) : "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
+                 "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]),
+                 "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]), "+v"(s[6]), "+v"(s[7])
+               :: "memory");
+  // Ordered after the wait (volatile asm keeps program order); ties the rest.
+  asm volatile("" : "+v"(s[8]), "+v"(s[9]), "+v"(s[10]), "+v"(s[11]), "+v"(s[12]), "+v"(s[13]), "+v"(s[14]), "+v"(s[15])
+               :: "memory");
+}
+
 // s_waitcnt vmcnt(0): this thread's vector memory operations, stores included,
 // have completed.  (GFX9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15.)
 __device__ __forceinline__ void wait_vmem_stores() {
@@ -92,13 +127,15 @@ __device__ __forceinline__ void wait_vmem_stores() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Eight fp16 values starting at column `col` of a row of length `d`.  VEC: the
-// row base is 16-byte aligned and d % 8 == 0, so one dwordx4 load serves.
+// Eight fp16 values starting at column `col` of a row of length `d`, zero past d.
+// VEC: the caller guarantees col + 8 <= d and a 16-byte aligned address, so one
+// unconditional dwordx4 load serves (the kernels use it when d equals their
+// padded width and every base pointer is 16-byte aligned).
 template <bool VEC>
 __device__ __forceinline__ u32x4 load_row8(const half_t* row, int col, int d) {
   if constexpr (VEC) {
-    if (col < d) return *reinterpret_cast<const u32x4*>(row + col);
-    return u32x4{0u, 0u, 0u, 0u};
+    (void)d;
+    return *reinterpret_cast<const u32x4*>(row + col);
   } else {
     half8_t h;
 #pragma unroll

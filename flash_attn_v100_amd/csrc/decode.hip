@@ -33,9 +33,21 @@ enum DecodeMode : int { kModeDecode = 0, kModeCB = 1, kModePaged = 2, kModeInt8 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = kDecWaves * 64;
 constexpr int kPage = 16;             // PAGE_BLOCK_SIZE of the paged cache
-constexpr int kMaxChunk = 8192;       // keys per split, upper bound
-constexpr int kChunkQuantum = 128;    // split boundaries are multiples of this
-constexpr int kTargetBlocks = 8192;   // aim for this many split workgroups
+// Split sizing.  The FA_DEC_* macros exist only to let a tuning sweep build
+// variants; the defaults are the shipped configuration.
+#ifndef FA_DEC_TARGET_BLOCKS
+#define FA_DEC_TARGET_BLOCKS 8192
+#endif
+#ifndef FA_DEC_CHUNK_QUANTUM
+#define FA_DEC_CHUNK_QUANTUM 128
+#endif
+constexpr int kMaxChunk = 8192;                        // keys per split, upper bound
+constexpr int kChunkQuantum = FA_DEC_CHUNK_QUANTUM;    // split boundaries are multiples of this
+constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many split workgroups
+// The paged kernel stages each split's page ids in LDS before its first load,
+// one extra memory round trip per split, so it prefers fewer, longer splits.
+constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / 4;
+constexpr int kMaxSplits = 128;       // splits per sequence, upper bound
 
 struct DecodeParams {
   const half_t* q;
@@ -87,12 +99,24 @@ __device__ __forceinline__ void quant8(u32x4 raw, float inv, int& lo, int& hi) {
   hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
 }
 
+// Per-wave LDS scratch used to hand probabilities from the MFMA layout (lane =
+// key) to the row layout (lanes = one key's columns).
+template <int GB>
+struct PExchange {
+  static constexpr int kPad = GB < 4 ? 4 : GB;
+};
+
 template <int DP, int GB, int MODE, bool VEC>
 __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParams p) {
-  constexpr int LPR = DP / 8;       // lanes per key row
-  constexpr int RPW = 64 / LPR;     // rows per wave per load instruction
-  constexpr int U = 8;              // load instructions in flight per tile
-  constexpr int TILE = RPW * U;     // keys per wave per iteration
+  constexpr int NC = DP / 32;                 // 32-column slices of the QK^T product
+  constexpr int LPR = DP / 8;                 // lanes per key row in the row layout
+  constexpr int RPW = 64 / LPR;               // rows covered by one row-layout load
+  constexpr int T16 = DP == 256 ? 1 : 2;      // 16-key MFMA tiles per iteration
+  constexpr int TK = 16 * T16;                // keys per wave per iteration
+  constexpr int UV = TK / RPW;                // row-layout V loads per lane per iteration
+  constexpr int GP = PExchange<GB>::kPad;     // padded heads per key in the exchange
+  constexpr float kRescaleSlack = 8.0f;       // log2 headroom before the max is refreshed
+  static_assert(TK % RPW == 0, "tile");
 
   const int S = p.num_splits;
   const int split = blockIdx.x % S;
@@ -105,10 +129,15 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   const int D = p.D;
   const int G = p.G;
   const int g_base = hg * GB;
+  const int g_valid = min(GB, G - g_base);  // heads of this group that exist
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  // MFMA layout: lane = (key l16 of a 16-key tile, quarter q)
+  const int l16 = lane & 15;
+  const int q4 = lane >> 4;
+  // row layout: lane = (row group rg, 8 columns at col)
   const int rg = lane / LPR;
   const int col = (lane % LPR) * 8;
 
@@ -122,7 +151,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     if (L <= 0 && split == 0) {
       for (int i = tid; i < GB * D; i += kDecThreads) {
         const int g = i / D, d = i % D;
-        if (g_base + g < G) {
+        if (g < g_valid) {
           const int h = hkv * G + g_base + g;
           p.o[(static_cast<size_t>(b) * p.H_Q + h) * D + d] = static_cast<half_t>(__builtin_nanf(""));
         }
@@ -150,158 +179,255 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     __syncthreads();
   }
 
-  const size_t kv_head_base =
-      (static_cast<size_t>(b) * p.H_KV + hkv) * static_cast<size_t>(p.N) * D;
-  auto row_off = [&](int t) -> size_t {
-    if constexpr (MODE == kModePaged) {
-      const int pg = s_pages[(t - k0) >> 4];
-      return ((static_cast<size_t>(pg) * p.H_KV + hkv) * kPage + (t & (kPage - 1))) * D;
-    } else {
-      return kv_head_base + static_cast<size_t>(t) * D;
-    }
+  // Row addressing.  Contiguous caches: one base per (b, h_kv) plus a 32-bit row
+  // offset.  Paged cache: a 16-key MFMA tile and each row-layout load both lie
+  // inside one page, so the page base is wave-uniform; rows past k1 inside the
+  // last page are real page memory (their scores are masked), and page slots
+  // past the split's last page are clamped to it.
+  const size_t kv_head_base = (static_cast<size_t>(b) * p.H_KV + hkv) * static_cast<size_t>(p.N) * D;
+  const int npages = (k1 - k0 + kPage - 1) / kPage;
+  auto page_base = [&](int t) -> size_t {  // t: any key of the page, t >= k0
+    const int slot = min((t - k0) >> 4, npages - 1);
+    const int pg = __builtin_amdgcn_readfirstlane(s_pages[slot]);
+    return (static_cast<size_t>(pg) * p.H_KV + hkv) * kPage * D;
   };
 
-  // ---- query fragments (this lane's 8 columns of each of the GB heads) ----
-  uint32_t qf[GB][4];
-  int qi[GB][2];
-  float qsc[GB];
-  float inv_ks = 0.0f, ks = 0.0f;
+  // ---- query fragments: MFMA A operand, lane holds head l16, columns 32c + 8*q4 .. +8 ----
+  const int hq_lane = hkv * G + g_base + l16;  // head of this lane's A row
+  const bool row_ok = l16 < g_valid;
+  half8_t qa[NC];
+  int qi8[NC][2];
+  float qsc[4];  // INT8: q scale of the heads whose scores this lane holds (g = 4*q4 + r)
+  float ks = 0.0f, inv_ks = 0.0f;
   if constexpr (MODE == kModeInt8) {
     ks = p.k_scale[static_cast<size_t>(b) * p.H_KV + hkv];
     inv_ks = 1.0f / ks;
-  }
 #pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    const bool hv = g_base + g < G;
-    const int h = hkv * G + g_base + g;
-    u32x4 x = u32x4{0u, 0u, 0u, 0u};
-    if (hv) x = load_row8<VEC>(p.q + (static_cast<size_t>(b) * p.H_Q + h) * D, col, D);
-    if constexpr (MODE == kModeInt8) {
-      const float qs = hv ? p.q_scale[static_cast<size_t>(b) * p.H_Q + h] : 1.0f;
-      qsc[g] = qs;
-      quant8(x, 1.0f / qs, qi[g][0], qi[g][1]);
-      if (!hv) qi[g][0] = qi[g][1] = 0;
-    } else {
-      qf[g][0] = x.x; qf[g][1] = x.y; qf[g][2] = x.z; qf[g][3] = x.w;
+    for (int r = 0; r < 4; ++r) {
+      const int g = 4 * q4 + r;
+      qsc[r] = g < g_valid ? p.q_scale[static_cast<size_t>(b) * p.H_Q + hkv * G + g_base + g] : 1.0f;
+    }
+  }
+  {
+    const half_t* qrow = p.q + (static_cast<size_t>(b) * p.H_Q + (row_ok ? hq_lane : 0)) * D;
+    const float inv_qs = (MODE == kModeInt8 && row_ok)
+                             ? 1.0f / p.q_scale[static_cast<size_t>(b) * p.H_Q + hq_lane] : 1.0f;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      u32x4 x = u32x4{0u, 0u, 0u, 0u};
+      if (row_ok) x = load_row8<VEC>(qrow, 32 * c + 8 * q4, D);
+      qa[c] = __builtin_bit_cast(half8_t, x);
+      if constexpr (MODE == kModeInt8) quant8(x, inv_qs, qi8[c][0], qi8[c][1]);
     }
   }
 
-  float m[GB], l[GB], acc[GB][8];
+  // Running state.  mu[r]: max (log2 domain) used for head g = 4*q4 + r, uniform
+  // across the 16 key lanes of quarter q4.  lpart[r]: this lane's partial sum.
+  float mu[4], lpart[4];
 #pragma unroll
-  for (int g = 0; g < GB; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.0f;
+  for (int r = 0; r < 4; ++r) {
+    mu[r] = kNegBig;
+    lpart[r] = 0.0f;
+  }
+  float acc[GB][8];
+#pragma unroll
+  for (int g = 0; g < GB; ++g)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
-  }
 
-  for (int t0 = k0 + wave * TILE; t0 < k1; t0 += kDecWaves * TILE) {
-    u32x4 kf[U], vf[U];
-    bool valid[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * RPW + rg;
-      valid[u] = t < k1;
-      kf[u] = u32x4{0u, 0u, 0u, 0u};
-      if (valid[u]) kf[u] = load_row8<VEC>(p.k + row_off(t), col, D);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int t = t0 + u * RPW + rg;
-      vf[u] = u32x4{0u, 0u, 0u, 0u};
-      if (valid[u]) vf[u] = load_row8<VEC>(p.v + row_off(t), col, D);
-    }
+  __shared__ __attribute__((aligned(16))) float s_p[kDecWaves][TK][GP];
+  __shared__ float s_alpha[kDecWaves][GP];
+  const int klast = k1 - 1;
 
-    float s[U][GB];
+  // One iteration's K (MFMA layout) and V (row layout) registers.
+  struct Tile {
+    u32x4 k[T16][NC];
+    u32x4 v[UV];
+  };
+  // -- loads: rows past k1 are clamped to k1-1 (always valid memory) and their
+  //    scores are masked in compute_tile.
+  auto load_tile = [&](Tile& T, int t0) {
+    if constexpr (MODE == kModePaged) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+      for (int tt = 0; tt < T16; ++tt) {
+        const half_t* kr = p.k + page_base(t0 + 16 * tt) + l16 * D;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) T.k[tt][c] = load_row8<VEC>(kr, 32 * c + 8 * q4, D);
+      }
+#pragma unroll
+      for (int u = 0; u < UV; ++u) {
+        const int t = t0 + u * RPW;  // RPW divides 16: all rows of this load share a page
+        T.v[u] = load_row8<VEC>(p.v + page_base(t) + ((t + rg) & (kPage - 1)) * D, col, D);
+      }
+    } else {
+      const half_t* kh = p.k + kv_head_base;
+      const half_t* vh = p.v + kv_head_base;
+#pragma unroll
+      for (int tt = 0; tt < T16; ++tt) {
+        const int t = min(t0 + 16 * tt + l16, klast);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) T.k[tt][c] = load_row8<VEC>(kh + t * D, 32 * c + 8 * q4, D);
+      }
+#pragma unroll
+      for (int u = 0; u < UV; ++u) {
+        const int t = min(t0 + u * RPW + rg, klast);
+        T.v[u] = load_row8<VEC>(vh + t * D, col, D);
+      }
+    }
+  };
+
+  auto compute_tile = [&](const Tile& T, int t0) {
+    // -- scores S[g = 4*q4 + r][key = l16] for each 16-key tile
+    float s[T16][4];
+#pragma unroll
+    for (int tt = 0; tt < T16; ++tt) {
+      float4_t sc;
       if constexpr (MODE == kModeInt8) {
-        int klo, khi;
-        quant8(kf[u], inv_ks, klo, khi);
+        typedef int int4v __attribute__((ext_vector_type(4)));
+        int4v ci = {0, 0, 0, 0};
 #pragma unroll
-        for (int g = 0; g < GB; ++g) {
-          int di = __builtin_amdgcn_sdot4(qi[g][0], klo, 0, false);
-          di = __builtin_amdgcn_sdot4(qi[g][1], khi, di, false);
-          di = group_sum_i<LPR>(di);
-          const float sc = static_cast<float>(di) * qsc[g] * ks * p.scale;
-          s[u][g] = valid[u] ? sc * kLog2e : -INFINITY;
+        for (int c = 0; c < NC; c += 2) {
+          int k0lo, k0hi, k1lo, k1hi;
+          quant8(T.k[tt][c], inv_ks, k0lo, k0hi);
+          quant8(T.k[tt][c + 1], inv_ks, k1lo, k1hi);
+          const int4v av = {qi8[c][0], qi8[c][1], qi8[c + 1][0], qi8[c + 1][1]};
+          const int4v bv = {k0lo, k0hi, k1lo, k1hi};
+          ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, ci, 0, 0, 0);
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          sc[r] = static_cast<float>(ci[r]) * qsc[r] * ks * p.scale * kLog2e;
       } else {
+        sc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int g = 0; g < GB; ++g) {
-          float d = dot2(qf[g][0], kf[u].x, 0.0f);
-          d = dot2(qf[g][1], kf[u].y, d);
-          d = dot2(qf[g][2], kf[u].z, d);
-          d = dot2(qf[g][3], kf[u].w, d);
-          d = group_sum<LPR>(d);
-          s[u][g] = valid[u] ? d * p.scale_log2 : -INFINITY;
+        for (int c = 0; c < NC; ++c)
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[c], __builtin_bit_cast(half8_t, T.k[tt][c]), sc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] *= p.scale_log2;
+      }
+      const bool key_ok = t0 + 16 * tt + l16 < k1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = key_ok && (4 * q4 + r < g_valid);
+        s[tt][r] = ok ? sc[r] : -INFINITY;
+      }
+    }
+
+    // -- lazy max refresh: only when a score exceeds the max in use by 2^8
+    bool grow = false;
+#pragma unroll
+    for (int tt = 0; tt < T16; ++tt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) grow |= s[tt][r] > mu[r] + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      float alpha[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float mx = s[0][r];
+#pragma unroll
+        for (int tt = 1; tt < T16; ++tt) mx = fmaxf(mx, s[tt][r]);
+        mx = fmaxf(mx, dpp_mov<kDppQuadXor1>(mx));
+        mx = fmaxf(mx, dpp_mov<kDppQuadXor2>(mx));
+        mx = fmaxf(mx, dpp_mov<kDppRowHalfMirror>(mx));
+        mx = fmaxf(mx, dpp_mov<kDppRowMirror>(mx));
+        const float mn = fmaxf(mu[r], mx);
+        alpha[r] = fast_exp2(mu[r] - mn);
+        mu[r] = mn;
+        lpart[r] *= alpha[r];
+      }
+      // hand alpha to the row layout
+      if (l16 == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * q4 + r < GP) s_alpha[wave][4 * q4 + r] = alpha[r];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int g = 0; g < GB; ++g) {
+        const float a = s_alpha[wave][g];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] *= a;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+
+    // -- probabilities: exp, partial sums, and hand-off to the row layout
+#pragma unroll
+    for (int tt = 0; tt < T16; ++tt) {
+      float pr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = fast_exp2(s[tt][r] - mu[r]);
+        lpart[r] += pr[r];
+      }
+      if (4 * q4 < GP) {
+        float* dst = &s_p[wave][16 * tt + l16][4 * q4];
+        if constexpr (GP >= 4) {
+          *reinterpret_cast<float4_t*>(dst) = float4_t{pr[0], pr[1], pr[2], pr[3]};
         }
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 
-    float vv[U][8];
+    // -- O += P V in the row layout
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      half8_t h = __builtin_bit_cast(half8_t, vf[u]);
+    for (int u = 0; u < UV; ++u) {
+      const int kl = u * RPW + rg;  // key index inside this iteration's tile
+      float pv[GP];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) vv[u][j] = static_cast<float>(h[j]);
-    }
-
-#pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      float mt = s[0][g];
-#pragma unroll
-      for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u][g]);
-      const float mn = fmaxf(m[g], mt);
-      const float alpha = fast_exp2(m[g] - mn);
-      m[g] = mn;
-      l[g] *= alpha;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] *= alpha;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float pu = fast_exp2(s[u][g] - mn);
-        l[g] += pu;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pu, vv[u][j], acc[g][j]);
+      for (int g4 = 0; g4 < GP; g4 += 4) {
+        const float4_t x = *reinterpret_cast<const float4_t*>(&s_p[wave][kl][g4]);
+        pv[g4] = x[0]; pv[g4 + 1] = x[1]; pv[g4 + 2] = x[2]; pv[g4 + 3] = x[3];
       }
+      const half8_t vh = __builtin_bit_cast(half8_t, T.v[u]);
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pv[g], static_cast<float>(vh[j]), acc[g][j]);
     }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  const int stride = kDecWaves * TK;
+  for (int t0 = k0 + wave * TK; t0 < k1; t0 += stride) {
+    Tile A;
+    load_tile(A, t0);
+    compute_tile(A, t0);
   }
 
-  // ---- merge the RPW row-group states of this wave ----
+  // ---- wave-level reduction: all lanes of a wave share mu, so plain sums ----
 #pragma unroll
-  for (int off = LPR; off < 64; off <<= 1) {
+  for (int r = 0; r < 4; ++r) lpart[r] = group_sum<16>(lpart[r]);
 #pragma unroll
-    for (int g = 0; g < GB; ++g) {
-      const float mo = __shfl_xor(m[g], off, 64);
-      const float lo = __shfl_xor(l[g], off, 64);
-      const float mn = fmaxf(m[g], mo);
-      const float a = fast_exp2(m[g] - mn);
-      const float c = fast_exp2(mo - mn);
-      l[g] = l[g] * a + lo * c;
+  for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float ao = __shfl_xor(acc[g][j], off, 64);
-        acc[g][j] = acc[g][j] * a + ao * c;
-      }
-      m[g] = mn;
-    }
-  }
+    for (int g = 0; g < GB; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] += __shfl_xor(acc[g][j], off, 64);
 
-  // ---- merge the waves through LDS and write ----
-  __shared__ float s_m[kDecWaves][GB];
-  __shared__ float s_l[kDecWaves][GB];
+  // ---- merge the waves through LDS ----
+  __shared__ float s_m[kDecWaves][GP];
+  __shared__ float s_l[kDecWaves][GP];
   __shared__ float s_acc[kDecWaves][GB][DP];
+  if (l16 == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int g = 4 * q4 + r;
+      if (g < GP) {
+        s_m[wave][g] = mu[r];
+        s_l[wave][g] = lpart[r];
+      }
+    }
+  }
   if (rg == 0) {
 #pragma unroll
-    for (int g = 0; g < GB; ++g) {
+    for (int g = 0; g < GB; ++g)
 #pragma unroll
       for (int j = 0; j < 8; ++j) s_acc[wave][g][col + j] = acc[g][j];
-      if (lane == 0) {
-        s_m[wave][g] = m[g];
-        s_l[wave][g] = l[g];
-      }
-    }
   }
   __syncthreads();
 
@@ -312,7 +438,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 
   for (int i = tid; i < GB * DP; i += kDecThreads) {
     const int g = i / DP, d = i % DP;
-    if (g_base + g >= G || d >= D) continue;
+    if (g >= g_valid || d >= D) continue;
     float mx = s_m[0][g];
 #pragma unroll
     for (int w = 1; w < kDecWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
@@ -353,22 +479,92 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   __syncthreads();
   if (!s_last) return;
 
-  for (int i = tid; i < GB * DP; i += kDecThreads) {
-    const int g = i / DP, d = i % DP;
-    if (g_base + g >= G || d >= D) continue;
-    const int h = hkv * G + g_base + g;
-    const size_t bh = static_cast<size_t>(b) * p.H_Q + h;
-    const float* lse = p.ws_lse + bh * S;
-    const float* po = p.ws_o + bh * S * DP;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < sb; ++sp) mx = fmaxf(mx, load_coherent(&lse[sp]));
-    float num = 0.0f, den = 0.0f;
-    for (int sp = 0; sp < sb; ++sp) {
-      const float w = fast_exp2(load_coherent(&lse[sp]) - mx);
-      den += w;
-      num += w * load_coherent(&po[static_cast<size_t>(sp) * DP + d]);
+  // Merge the sb partials of each head in one batch of coherent loads: thread
+  // (column group c, phase ph) reads the lse and 4 output columns of splits
+  // ph, ph + NPH, ... together, keeps its own running max, and the phases
+  // meet in LDS with a rescale -- one memory round trip for the whole merge.
+  constexpr int NP = GB * DP / 4;                                  // float4 columns
+  constexpr int NPH = NP >= kDecThreads ? 1 : kDecThreads / NP;    // split phases
+  constexpr int NB = 16;                                           // splits per batch (load_coherent_batch16)
+  __shared__ float4_t s_num[NPH][NPH > 1 ? NP : 1];
+  __shared__ float s_mx[NPH][NPH > 1 ? NP : 1];
+  __shared__ float s_den[NPH][NPH > 1 ? NP : 1];
+  struct Part {
+    float4_t num;
+    float mx, den;
+  };
+  auto column_merge = [&](int c, int ph) -> Part {
+    Part r = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, -INFINITY, 0.0f};
+    const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
+    if (g >= g_valid || d4 >= D) return r;
+    const size_t bh = static_cast<size_t>(b) * p.H_Q + hkv * G + g_base + g;
+    const float* po = p.ws_o + bh * S * DP + d4;
+    const float* pl = p.ws_lse + bh * S;
+    for (int sp = ph; sp < sb; sp += NB * NPH) {
+      float lv[NB];
+      float4_t v[NB];
+      int qs[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) qs[j] = min(sp + j * NPH, sb - 1);  // in-range address, masked below
+      load_coherent_batch16(po, DP, pl, qs, v, lv);
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        if (sp + j * NPH >= sb) {
+          lv[j] = -INFINITY;
+          v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      float m = r.mx;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) m = fmaxf(m, lv[j]);
+      const float a = fast_exp2(r.mx - m);
+      r.num *= a;
+      r.den *= a;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const float w = fast_exp2(lv[j] - m);
+        r.den += w;
+        r.num += w * v[j];
+      }
+      r.mx = m;
     }
-    p.o[bh * D + d] = static_cast<half_t>(num / den);
+    return r;
+  };
+  auto store_out = [&](int c, float4_t o) {
+    const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
+    if (g >= g_valid || d4 >= D) return;
+    half_t* op = p.o + (static_cast<size_t>(b) * p.H_Q + hkv * G + g_base + g) * D + d4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (d4 + j < D) op[j] = static_cast<half_t>(o[j]);
+  };
+  if constexpr (NPH == 1) {
+    for (int c = tid; c < NP; c += kDecThreads) {
+      const Part r = column_merge(c, 0);
+      store_out(c, r.num / r.den);
+    }
+  } else {
+    const int c = tid % NP, ph = tid / NP;
+    if (ph < NPH) {
+      const Part r = column_merge(c, ph);
+      s_num[ph][c] = r.num;
+      s_mx[ph][c] = r.mx;
+      s_den[ph][c] = r.den;
+    }
+    __syncthreads();
+    if (tid < NP) {
+      float m = s_mx[0][tid];
+#pragma unroll
+      for (int q = 1; q < NPH; ++q) m = fmaxf(m, s_mx[q][tid]);
+      float4_t num = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      float den = 0.0f;
+#pragma unroll
+      for (int q = 0; q < NPH; ++q) {
+        const float w = s_mx[q][tid] == -INFINITY ? 0.0f : fast_exp2(s_mx[q][tid] - m);
+        num += w * s_num[q][tid];
+        den += w * s_den[q][tid];
+      }
+      store_out(tid, num / den);
+    }
   }
   // Leave the counter at zero for the next call on this workspace.
   if (tid == 0) atomicExch(&p.counters[slot], 0u);
@@ -382,17 +578,21 @@ struct DecodePlan {
 };
 
 static int pick_dp(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
-static int pick_gb(int g) { return g <= 1 ? 1 : (g <= 2 ? 2 : (g <= 4 ? 4 : 8)); }
+// Query heads per workgroup: one 16-row MFMA tile holds up to 16 heads of a group.
+static int pick_gb(int g) { return g <= 1 ? 1 : (g <= 2 ? 2 : (g <= 4 ? 4 : (g <= 8 ? 8 : 16))); }
 
-static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D) {
+static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int target_blocks) {
   DecodePlan pl;
   const int G = H_Q / H_KV;
   pl.dp = pick_dp(D);
   pl.gb = pick_gb(G);
   pl.num_hg = ceil_div(G, pl.gb);
   const long long units = static_cast<long long>(B) * H_KV * pl.num_hg;
-  long long want = (static_cast<long long>(max_len > 0 ? max_len : 1) * units + kTargetBlocks - 1) / kTargetBlocks;
+  long long want = (static_cast<long long>(max_len > 0 ? max_len : 1) * units + target_blocks - 1) / target_blocks;
   long long chunk = ((want + kChunkQuantum - 1) / kChunkQuantum) * kChunkQuantum;
+  // at most kMaxSplits splits per sequence
+  const long long min_chunk = (static_cast<long long>(max_len) + kMaxSplits - 1) / kMaxSplits;
+  if (chunk < min_chunk) chunk = ((min_chunk + kChunkQuantum - 1) / kChunkQuantum) * kChunkQuantum;
   if (chunk < kChunkQuantum) chunk = kChunkQuantum;
   if (chunk > kMaxChunk) chunk = kMaxChunk;
   pl.chunk = static_cast<int>(chunk);
@@ -437,7 +637,8 @@ static void dispatch_gb(int gb, const DecodeParams& p, int blocks, hipStream_t s
     case 1: launch_split<DP, 1, MODE, VEC>(p, blocks, st); break;
     case 2: launch_split<DP, 2, MODE, VEC>(p, blocks, st); break;
     case 4: launch_split<DP, 4, MODE, VEC>(p, blocks, st); break;
-    default: launch_split<DP, 8, MODE, VEC>(p, blocks, st); break;
+    case 8: launch_split<DP, 8, MODE, VEC>(p, blocks, st); break;
+    default: launch_split<DP, 16, MODE, VEC>(p, blocks, st); break;
   }
 }
 
@@ -465,12 +666,15 @@ static int check_common(const char* fn, int B, int H_Q, int H_KV, int D) {
 
 template <int MODE>
 static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, size_t ws_bytes, void* stream) {
-  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D);
+  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D,
+                                  MODE == kModePaged ? kTargetBlocksPaged : kTargetBlocks);
   const WorkspaceLayout wl = plan_layout(pl, p.B, p.H_Q, p.H_KV);
   const size_t need = wl.total;
   if (need > 0 && (ws == nullptr || ws_bytes < need))
     return set_error(FA_ERR_WORKSPACE, "%s: workspace of %zu bytes required, %zu given", fn, need, ws_bytes);
   if (p.B == 0) return FA_OK;
+  if (pl.splits > kMaxSplits)
+    return set_error(FA_ERR_UNSUPPORTED, "%s: %d keys per sequence exceed %d", fn, max_len, kMaxSplits * kMaxChunk);
   p.G = p.H_Q / p.H_KV;
   p.chunk = pl.chunk;
   p.num_splits = pl.splits;
@@ -483,7 +687,8 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
     p.ws_lse = reinterpret_cast<float*>(base + wl.lse);
     p.ws_o = reinterpret_cast<float*>(base + wl.o);
   }
-  const bool vec = (p.D % 8 == 0) && aligned16(p.q) && aligned16(p.k) && aligned16(p.v);
+  // Vector path: D fills the padded width exactly and every row starts 16-byte aligned.
+  const bool vec = (p.D == pl.dp) && aligned16(p.q) && aligned16(p.k) && aligned16(p.v);
   const long long units = static_cast<long long>(p.B) * p.H_KV * pl.num_hg;
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (long long u0 = 0; u0 < units; u0 += static_cast<long long>(kCounterSlots)) {
@@ -502,7 +707,8 @@ using namespace fa;
 
 extern "C" size_t fa_decode_workspace_size(int B, int H_Q, int H_KV, int max_len, int D) {
   if (B <= 0 || H_Q <= 0 || H_KV <= 0 || D <= 0 || D > 256 || H_Q % H_KV != 0) return 0;
-  return plan_layout(make_plan(B, H_Q, H_KV, max_len, D), B, H_Q, H_KV).total;
+  // The contiguous plan has the most splits, so its size covers every mode.
+  return plan_layout(make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocks), B, H_Q, H_KV).total;
 }
 
 extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void* o, int B, int H_Q,

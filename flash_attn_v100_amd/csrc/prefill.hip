@@ -288,7 +288,8 @@ extern "C" int fa_prefill_fp16(const void* q, const void* k, const void* v, void
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D; p.G = H_Q / H_KV;
   p.causal = causal ? 1 : 0;
   p.scale_log2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
-  const bool vec = (D % 8 == 0) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  // Vector path: D fills the padded width exactly and every row starts 16-byte aligned.
+  const bool vec = (D == 64 || D == 128 || D == 256) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   dim3 grid(ceil_div(N, kBQ), H_Q, B);
   dispatch_prefill<false>(D, vec, grid, p, static_cast<hipStream_t>(stream));
   return check_launch(fn);
@@ -317,7 +318,7 @@ extern "C" int fa_varlen_prefill_fp16(const void* q, const void* k, const void* 
   p.row_limit = row_limit;
   p.causal = causal ? 1 : 0;
   p.scale_log2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
-  const bool vec = (D % 8 == 0) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  const bool vec = (D == 64 || D == 128 || D == 256) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   // Rows past min(row_limit, total) are never computed, so the grid covers that many.
   const int rows_max = row_limit < total ? row_limit : total;
   dim3 grid(ceil_div(rows_max, kBQ), H, batch);
