@@ -1,18 +1,34 @@
 // MFMA-tiled online-softmax prefill for gfx950 (dense MHA/GQA and packed varlen).
 //
-// Workgroup = 4 waves = 128 query rows (32 per wave) of one (batch, head);
-// the KV sequence is walked in 64-key tiles staged in LDS:
-//   sK  [64][DP + 8]      key-major, read as the A operand of S^T = K Q^T
-//   sVt [DP][64 + 8]      V transposed, read as the A operand of O^T = V^T P^T
-// Both products use v_mfma_f32_32x32x16_f16.  Computing the transposed scores
-// puts one query row per lane (lane l owns query l%32 and 16 keys of each 32-key
-// block), so the row max needs a single cross-lane exchange (lanes l, l^32),
-// the row sum stays lane-partial until the end, and the fp32 S accumulator,
-// converted to fp16, is directly the B operand of the PV product: the key order
-// inside each 16-wide k-slice of that MFMA is chosen to match the accumulator
-// layout, and sVt is read in that same order (two 8-byte reads per operand).
-// The next tile's K/V global loads are issued before the current tile's MFMAs
-// so their HBM latency overlaps compute.
+// Workgroup = 4 waves; each wave owns RW = 64 query rows (32 when D > 128) of one
+// (batch, head), so a workgroup covers 4*RW rows.  The KV sequence is walked in
+// BK-key tiles (64 keys for D <= 64, 32 above, for the register budget) staged
+// in LDS, both row-major:
+//   sK [BK][DP + 8]    read (16 B per lane) as the A operand of S^T = K Q^T
+//   sV [BK][DP + 32]   read with ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T
+// Both products use v_mfma_f32_32x32x16_f16, and each K / V operand read from LDS
+// feeds RB = RW/32 MFMAs (one per 32-row query block), halving LDS traffic per
+// FLOP against one block per wave.
+//
+// S^T = K Q^T puts one query row per lane (lane l owns query l%32 of each block
+// and 16 keys of each 32-key block): the row max needs one exchange (lanes l,
+// l^32) and the row sum stays lane-partial until the end.  The fp32 S^T
+// accumulator, converted to fp16, is directly the B operand of the PV product:
+// inside each 16-key slice lane half h holds keys {4h..4h+3, 8+4h..8+4h+3}, and
+// the transposing LDS read delivers V in exactly that key order (one read per
+// 4-key run: 16 source lanes read a 4-key x 16-column block of row-major V and
+// lane i receives the 4 keys of column i).  The V row pitch is 64 bytes past a
+// multiple of 256, which makes those reads, and the 16-byte row writes, free of
+// bank conflicts.
+//
+// Online softmax with lazy rescaling: the max used for the exponentials is only
+// refreshed when a tile's max exceeds it by 2^8 (wave-uniform test), so the O
+// accumulators are rarely touched outside the MFMAs.  Only tiles that cross
+// the causal diagonal or the sequence end run the masked variant; each wave
+// stops at its own diagonal.  Work items are ordered heaviest first across the
+// whole grid (all (batch, head) pairs of the last query tile, then the next).
+// For D <= 128 the next tile's K/V global loads are issued before the current
+// tile's MFMAs.
 #include <math.h>
 
 #include "capi_internal.h"
@@ -22,10 +38,8 @@ namespace fa {
 
 constexpr int kPreWaves = 4;
 constexpr int kPreThreads = kPreWaves * 64;
-constexpr int kBQ = 32 * kPreWaves;  // query rows per workgroup
-constexpr int kBK = 64;              // keys per tile
-constexpr int kKPad = 8;             // halves of padding per sK row
-constexpr int kVPad = 8;             // halves of padding per sVt row
+constexpr int kKPad = 8;    // halves of padding per sK row
+constexpr int kVPad = 32;   // halves of padding per sV row (pitch = 64 B mod 256 B)
 
 struct PrefillParams {
   const half_t* q;
@@ -36,39 +50,65 @@ struct PrefillParams {
   int B, H_Q, H_KV, N, D, G;
   int total, row_limit;       // varlen only
   int causal;
-  float scale_log2;
+  int qtiles;                 // query tiles per (batch, head) in the grid
+  float scale_log2;           // (1/sqrt(D)) * log2(e)
 };
 
-template <int N>
-struct HalfVec;
-template <>
-struct HalfVec<2> { typedef half2_t type; };
-template <>
-struct HalfVec<4> { typedef half4_t type; };
-template <>
-struct HalfVec<8> { typedef half8_t type; };
+template <int DP>
+struct PrefillShape {
+  static constexpr int RB = DP <= 64 ? 2 : 1;   // 32-row query blocks per wave
+  static constexpr int RW = 32 * RB;            // query rows per wave
+  static constexpr int BQ = kPreWaves * RW;     // query rows per workgroup
+  static constexpr int BK = DP <= 128 ? 64 : 32;  // keys per tile (register budget)
+};
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+template <bool B>
+struct MaskedTag {
+  static constexpr bool value = B;
+};
+
+// Four fp16 values of V for the PV A operand: keys base..base+3 of column
+// col0 + (lane % 16), via the transposing LDS read (see the file comment).
+__device__ __forceinline__ half4_t read_v_tr(const half_t* sV, int pitch, int key_base, int col0, int lane) {
+  const int s = lane & 15;
+  const half_t* src = sV + (key_base + (s >> 2)) * pitch + col0 + 4 * (s & 3);
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(__builtin_amdgcn_readfirstlane(0) + src));
+  return __builtin_bit_cast(half4_t, v);
+}
 
 template <int DP, bool VARLEN, bool VEC>
 __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
-  constexpr int KK = DP / 16;         // 16-wide d slices of the QK^T product
-  constexpr int DB = DP / 32;         // 32-row d blocks of the PV product
-  constexpr int CPR = DP / 8;         // 16-byte chunks per row
-  constexpr int R = kBK * CPR / kPreThreads;  // consecutive key rows per staging thread
-  constexpr int KPITCH = DP + kKPad;
-  constexpr int VPITCH = kBK + kVPad;
-  typedef typename HalfVec<R>::type halfR;
+  using Shape = PrefillShape<DP>;
+  constexpr int RB = Shape::RB;
+  constexpr int RW = Shape::RW;
+  constexpr int BQ = Shape::BQ;
+  constexpr int kBK = Shape::BK;
+  constexpr int NBLK = kBK / 32;              // 32-key blocks per tile
+  constexpr int KK = DP / 16;                 // 16-wide d slices of QK^T
+  constexpr int DB = DP / 32;                 // 32-row d blocks of PV
+  constexpr int CPR = DP / 8;                 // 16-byte chunks per row
+  constexpr int RPT = kBK * CPR / kPreThreads;  // 16-byte chunks per thread per tile
+  constexpr int KP = DP + kKPad;
+  constexpr int VP = DP + kVPad;
+  constexpr float kRescaleSlack = 8.0f;
 
-  __shared__ __attribute__((aligned(16))) half_t sK[kBK * KPITCH];
-  __shared__ __attribute__((aligned(16))) half_t sVt[DP * VPITCH];
+  __shared__ __attribute__((aligned(16))) half_t sK[PrefillShape<DP>::BK * KP];
+  __shared__ __attribute__((aligned(16))) half_t sV[PrefillShape<DP>::BK * VP];
 
   const int D = p.D;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  // Heaviest work first: all (batch, head) pairs of the last query tile, then the next.
+  const int pairs = p.H_Q * p.B;
+  const int qt = p.qtiles - 1 - static_cast<int>(blockIdx.x / pairs);
+  const int rem = blockIdx.x % pairs;
+  const int h = rem % p.H_Q;
+  const int b = rem / p.H_Q;
   const int hk = h / p.G;
 
   // ---- sequence geometry ----
-  size_t q_base, k_base;     // element offsets of row 0, column 0 of this head
-  size_t q_stride, k_stride; // elements between consecutive rows
+  size_t q_base, k_base, stride;
   int seq_len, rows;
   if constexpr (VARLEN) {
     int s = p.cu_seqlens[b];
@@ -77,17 +117,16 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
     e = max(0, min(e, p.total));
     seq_len = e - s;
     rows = min(seq_len, p.row_limit);
-    q_stride = k_stride = static_cast<size_t>(p.H_Q) * D;
-    q_base = static_cast<size_t>(s) * q_stride + static_cast<size_t>(h) * D;
+    stride = static_cast<size_t>(p.H_Q) * D;
+    q_base = static_cast<size_t>(s) * stride + static_cast<size_t>(h) * D;
     k_base = q_base;
   } else {
     seq_len = rows = p.N;
-    q_stride = k_stride = D;
+    stride = D;
     q_base = (static_cast<size_t>(b) * p.H_Q + h) * static_cast<size_t>(p.N) * D;
     k_base = (static_cast<size_t>(b) * p.H_KV + hk) * static_cast<size_t>(p.N) * D;
   }
-  // Heaviest (last) query tiles are dispatched first.
-  const int q0 = (gridDim.x - 1 - blockIdx.x) * kBQ;
+  const int q0 = qt * BQ;
   if (q0 >= rows) return;
 
   const int tid = threadIdx.x;
@@ -95,174 +134,216 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
   const int wave = tid >> 6;
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  const int qrow = q0 + wave * 32 + l32;  // query row owned by this lane
+  const int wq0 = q0 + wave * RW;  // first query row of this wave
 
   const half_t* __restrict__ qp = p.q + q_base;
   const half_t* __restrict__ kp = p.k + k_base;
   const half_t* __restrict__ vp = p.v + k_base;
 
-  // ---- Q fragments: B operand of S^T, lane holds q row l32, d = kk*16 + 8*hi .. +8 ----
-  half8_t qf[KK];
+  // ---- Q fragments: B operand of S^T; block rb, lane row wq0 + 32 rb + l32, d = 16 kk + 8 hi .. +8 ----
+  half8_t qf[RB][KK];
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    u32x4 x = u32x4{0u, 0u, 0u, 0u};
-    if (qrow < rows) x = load_row8<VEC>(qp + static_cast<size_t>(qrow) * q_stride, kk * 16 + 8 * hi, D);
-    qf[kk] = __builtin_bit_cast(half8_t, x);
+  for (int rb = 0; rb < RB; ++rb) {
+    const int qrow = wq0 + 32 * rb + l32;
+    const half_t* qr = qp + static_cast<size_t>(min(qrow, rows - 1)) * stride;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      u32x4 x = load_row8<VEC>(qr, kk * 16 + 8 * hi, D);
+      if (qrow >= rows) x = u32x4{0u, 0u, 0u, 0u};
+      qf[rb][kk] = __builtin_bit_cast(half8_t, x);
+    }
   }
 
-  const int kend = p.causal ? min(seq_len, q0 + kBQ) : seq_len;
-  const int ntiles = (kend + kBK - 1) / kBK;
+  // key ranges: the workgroup walks to its last wave's diagonal, each wave stops at its own
+  const int kend_wg = p.causal ? min(seq_len, q0 + BQ) : seq_len;
+  const int kend_w = p.causal ? min(seq_len, wq0 + RW) : seq_len;
+  const int ntiles = (kend_wg + kBK - 1) / kBK;
 
-  // staging assignment: chunk c of rows key0 .. key0+R-1
+  // staging: thread owns 16-byte chunk (tid % CPR) of rows (tid / CPR) + r * (256 / CPR)
+  constexpr int RSTEP = kPreThreads / CPR;
   const int sc = tid % CPR;
-  const int skey0 = (tid / CPR) * R;
-
-  u32x4 kreg[R], vreg[R];
+  const int srow = tid / CPR;
+  u32x4 kreg[RPT], vreg[RPT];
   auto fetch = [&](int kt) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int key = kt + skey0 + r;
-      kreg[r] = u32x4{0u, 0u, 0u, 0u};
-      vreg[r] = u32x4{0u, 0u, 0u, 0u};
-      if (key < seq_len) {
-        kreg[r] = load_row8<VEC>(kp + static_cast<size_t>(key) * k_stride, sc * 8, D);
-        vreg[r] = load_row8<VEC>(vp + static_cast<size_t>(key) * k_stride, sc * 8, D);
+    for (int r = 0; r < RPT; ++r) {
+      const int key = kt + srow + r * RSTEP;
+      const int kc = min(key, seq_len - 1);
+      kreg[r] = load_row8<VEC>(kp + static_cast<size_t>(kc) * stride, sc * 8, D);
+      vreg[r] = load_row8<VEC>(vp + static_cast<size_t>(kc) * stride, sc * 8, D);
+      if (key >= seq_len) {
+        kreg[r] = u32x4{0u, 0u, 0u, 0u};
+        vreg[r] = u32x4{0u, 0u, 0u, 0u};
       }
     }
   };
 
-  float16_t oacc[DB];
+  float16_t oacc[DB][RB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.0f;
-  float m_run = kNegBig;  // running max (log2 domain) of query qrow
-  float l_run = 0.0f;     // lane-partial running sum
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) oacc[db][rb][r] = 0.0f;
+  float m_run[RB], l_run[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    m_run[rb] = kNegBig;
+    l_run[rb] = 0.0f;
+  }
+  const float c = p.scale_log2;
 
-  if (ntiles > 0) fetch(0);
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int kt = t * kBK;
-    __syncthreads();  // previous tile's LDS reads are done
+  auto compute_tile = [&](const int kt, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    // ---- S^T = K Q^T ----
+    float16_t sacc[NBLK][RB];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      *reinterpret_cast<u32x4*>(&sK[(skey0 + r) * KPITCH + sc * 8]) = kreg[r];
-    {
-      half8_t vh[R];
+    for (int blk = 0; blk < NBLK; ++blk)
 #pragma unroll
-      for (int r = 0; r < R; ++r) vh[r] = __builtin_bit_cast(half8_t, vreg[r]);
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        halfR col;
+        for (int r = 0; r < 16; ++r) sacc[blk][rb][r] = 0.0f;
 #pragma unroll
-        for (int r = 0; r < R; ++r) col[r] = vh[r][j];
-        *reinterpret_cast<halfR*>(&sVt[(sc * 8 + j) * VPITCH + skey0]) = col;
+    for (int kk = 0; kk < KK; ++kk) {
+#pragma unroll
+      for (int blk = 0; blk < NBLK; ++blk) {
+        const half8_t a = *reinterpret_cast<const half8_t*>(&sK[(blk * 32 + l32) * KP + kk * 16 + 8 * hi]);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          sacc[blk][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[rb][kk], sacc[blk][rb], 0, 0, 0);
       }
     }
-    __syncthreads();
-    if (t + 1 < ntiles) fetch(kt + kBK);
-
-    // ---- S^T = K Q^T : two 32-key blocks ----
-    float16_t sacc[2];
+    // ---- softmax (lane owns query row wq0 + 32 rb + l32) ----
+    half8_t pf[RB][2 * NBLK];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+    for (int rb = 0; rb < RB; ++rb) {
+      if constexpr (MASKED) {
+        const int qrow = wq0 + 32 * rb + l32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) sacc[blk][r] = 0.0f;
+        for (int blk = 0; blk < NBLK; ++blk)
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const half8_t a = *reinterpret_cast<const half8_t*>(&sK[(blk * 32 + l32) * KPITCH + kk * 16 + 8 * hi]);
-        sacc[blk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kk], sacc[blk], 0, 0, 0);
+          for (int r = 0; r < 16; ++r) {
+            const int key = kt + blk * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+            const bool dead = key >= seq_len || (p.causal && key > qrow);
+            sacc[blk][rb][r] = dead ? -INFINITY : sacc[blk][rb][r];
+          }
       }
-    }
-
-    // ---- mask + online softmax (lane owns query qrow) ----
-    const bool need_mask = (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > q0 + wave * 32);
-    float mx = -INFINITY;
+      float mx = sacc[0][rb][0];
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+      for (int blk = 0; blk < NBLK; ++blk)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float s = sacc[blk][r] * p.scale_log2;
-        if (need_mask) {
-          const int key = kt + blk * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-          if (key >= seq_len || (p.causal && key > qrow)) s = -INFINITY;
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[blk][rb][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[rb] + kRescaleSlack) != 0) {
+        const float mn = fmaxf(m_run[rb], mx);
+        const float alpha = fast_exp2(m_run[rb] - mn);
+        m_run[rb] = mn;
+        l_run[rb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) oacc[db][rb][r] *= alpha;
+      }
+      const float mneg = -m_run[rb];
+      float ls = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2 * NBLK; ++i) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float e = fast_exp2(fmaf(sacc[i >> 1][rb][8 * (i & 1) + j], c, mneg));
+          ls += e;
+          pf[rb][i][j] = static_cast<half_t>(e);
         }
-        sacc[blk][r] = s;
-        mx = fmaxf(mx, s);
       }
+      l_run[rb] += ls;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    l_run *= alpha;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-
-    half8_t pf[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float e = fast_exp2(sacc[i >> 1][8 * (i & 1) + j] - m_new);
-        l_run += e;
-        pf[i][j] = static_cast<half_t>(e);
-      }
-    }
-
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const half_t* vrow = &sVt[(db * 32 + l32) * VPITCH];
+      const int col0 = db * 32 + 16 * ((lane >> 4) & 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half4_t lo = *reinterpret_cast<const half4_t*>(vrow + 16 * i + 4 * hi);
-        const half4_t hi4 = *reinterpret_cast<const half4_t*>(vrow + 16 * i + 8 + 4 * hi);
+      for (int i = 0; i < 2 * NBLK; ++i) {
+        const half4_t lo = read_v_tr(sV, VP, 16 * i + 4 * hi, col0, lane);
+        const half4_t hi4 = read_v_tr(sV, VP, 16 * i + 8 + 4 * hi, col0, lane);
         const half8_t a = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
-        oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[i], oacc[db], 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          oacc[db][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[rb][i], oacc[db][rb], 0, 0, 0);
       }
     }
+  };
+
+  // D > 128 has no registers to spare for a prefetched tile: it loads each tile
+  // at the top of its own iteration instead.
+  constexpr bool kPrefetch = DP <= 128;
+  if (kPrefetch && ntiles > 0) fetch(0);
+  for (int t = 0; t < ntiles; ++t) {
+    const int kt = t * kBK;
+    if (!kPrefetch) fetch(kt);
+    __syncthreads();  // previous tile's LDS reads are done
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int row = srow + r * RSTEP;
+      *reinterpret_cast<u32x4*>(&sK[row * KP + sc * 8]) = kreg[r];
+      *reinterpret_cast<u32x4*>(&sV[row * VP + sc * 8]) = vreg[r];
+    }
+    __syncthreads();
+    if (kPrefetch && t + 1 < ntiles) fetch(kt + kBK);
+    if (kt >= kend_w) continue;  // past this wave's diagonal (still joins the barriers)
+    const bool need_mask = (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > wq0);
+    if (need_mask) compute_tile(kt, MaskedTag<true>{});
+    else compute_tile(kt, MaskedTag<false>{});
   }
 
   // ---- finalize and store O[qrow][d] ----
-  l_run += __shfl_xor(l_run, 32, 64);
-  if (qrow >= rows) return;
-  const float inv = 1.0f / l_run;
-  half_t* op = p.o + q_base + static_cast<size_t>(qrow) * q_stride;
 #pragma unroll
-  for (int db = 0; db < DB; ++db) {
+  for (int rb = 0; rb < RB; ++rb) {
+    const float lt = l_run[rb] + __shfl_xor(l_run[rb], 32, 64);
+    const int qrow = wq0 + 32 * rb + l32;
+    if (qrow >= rows) continue;
+    const float inv = 1.0f / lt;
+    half_t* op = p.o + q_base + static_cast<size_t>(qrow) * stride;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int d0 = db * 32 + 8 * rr + 4 * hi;
-      half4_t hv;
+    for (int db = 0; db < DB; ++db) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) hv[j] = static_cast<half_t>(oacc[db][4 * rr + j] * inv);
-      if constexpr (VEC) {
-        if (d0 < D) *reinterpret_cast<half4_t*>(op + d0) = hv;
-      } else {
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = db * 32 + 8 * rr + 4 * hi;
+        half4_t hv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (d0 + j < D) op[d0 + j] = hv[j];
+        for (int j = 0; j < 4; ++j) hv[j] = static_cast<half_t>(oacc[db][rb][4 * rr + j] * inv);
+        if constexpr (VEC) {
+          *reinterpret_cast<half4_t*>(op + d0) = hv;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (d0 + j < D) op[d0 + j] = hv[j];
+        }
       }
     }
   }
 }
 
 template <int DP, bool VARLEN>
-static void launch_prefill(bool vec, dim3 grid, const PrefillParams& p, hipStream_t st) {
+static void launch_prefill(bool vec, int blocks, const PrefillParams& p, hipStream_t st) {
   if (vec)
-    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, true>), grid, dim3(kPreThreads), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, true>), dim3(blocks), dim3(kPreThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, false>), grid, dim3(kPreThreads), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, false>), dim3(blocks), dim3(kPreThreads), 0, st, p);
 }
 
+static int prefill_bq(int D) { return D <= 64 ? PrefillShape<64>::BQ : (D <= 128 ? PrefillShape<128>::BQ : PrefillShape<256>::BQ); }
+
+// Launches over qtiles * H_Q * B workgroups; returns FA_OK or an error code.
 template <bool VARLEN>
-static void dispatch_prefill(int D, bool vec, dim3 grid, const PrefillParams& p, hipStream_t st) {
-  if (D <= 64) launch_prefill<64, VARLEN>(vec, grid, p, st);
-  else if (D <= 128) launch_prefill<128, VARLEN>(vec, grid, p, st);
-  else launch_prefill<256, VARLEN>(vec, grid, p, st);
+static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, PrefillParams p, hipStream_t st) {
+  p.qtiles = ceil_div(rows_max, prefill_bq(D));
+  const long long blocks = static_cast<long long>(p.qtiles) * p.H_Q * p.B;
+  if (blocks > 0x7fffffffLL) return set_error(FA_ERR_UNSUPPORTED, "%s: problem too large for one launch", fn);
+  if (blocks == 0) return FA_OK;
+  if (D <= 64) launch_prefill<64, VARLEN>(vec, static_cast<int>(blocks), p, st);
+  else if (D <= 128) launch_prefill<128, VARLEN>(vec, static_cast<int>(blocks), p, st);
+  else launch_prefill<256, VARLEN>(vec, static_cast<int>(blocks), p, st);
+  return check_launch(fn);
 }
 
 }  // namespace fa
@@ -279,7 +360,6 @@ extern "C" int fa_prefill_fp16(const void* q, const void* k, const void* v, void
   if (D > 256) return set_error(FA_ERR_UNSUPPORTED, "%s: D=%d exceeds 256", fn, D);
   if (B == 0 || N == 0) return FA_OK;
   if (!q || !k || !v || !o) return set_error(FA_ERR_INVALID_ARG, "%s: null tensor pointer", fn);
-  if (B > 65535 || H_Q > 65535) return set_error(FA_ERR_UNSUPPORTED, "%s: B/H_Q exceed the grid limits", fn);
   PrefillParams p = {};
   p.q = static_cast<const half_t*>(q);
   p.k = static_cast<const half_t*>(k);
@@ -290,9 +370,7 @@ extern "C" int fa_prefill_fp16(const void* q, const void* k, const void* v, void
   p.scale_log2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
   // Vector path: D fills the padded width exactly and every row starts 16-byte aligned.
   const bool vec = (D == 64 || D == 128 || D == 256) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  dim3 grid(ceil_div(N, kBQ), H_Q, B);
-  dispatch_prefill<false>(D, vec, grid, p, static_cast<hipStream_t>(stream));
-  return check_launch(fn);
+  return dispatch_prefill<false>(fn, D, vec, N, p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fa_varlen_prefill_fp16(const void* q, const void* k, const void* v, void* o,
@@ -306,7 +384,6 @@ extern "C" int fa_varlen_prefill_fp16(const void* q, const void* k, const void* 
   if (D > 256) return set_error(FA_ERR_UNSUPPORTED, "%s: D=%d exceeds 256", fn, D);
   if (batch == 0 || total == 0 || row_limit == 0) return FA_OK;
   if (!q || !k || !v || !o || !cu_seqlens) return set_error(FA_ERR_INVALID_ARG, "%s: null pointer", fn);
-  if (batch > 65535 || H > 65535) return set_error(FA_ERR_UNSUPPORTED, "%s: batch/H exceed the grid limits", fn);
   PrefillParams p = {};
   p.q = static_cast<const half_t*>(q);
   p.k = static_cast<const half_t*>(k);
@@ -321,7 +398,5 @@ extern "C" int fa_varlen_prefill_fp16(const void* q, const void* k, const void* 
   const bool vec = (D == 64 || D == 128 || D == 256) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   // Rows past min(row_limit, total) are never computed, so the grid covers that many.
   const int rows_max = row_limit < total ? row_limit : total;
-  dim3 grid(ceil_div(rows_max, kBQ), H, batch);
-  dispatch_prefill<true>(D, vec, grid, p, static_cast<hipStream_t>(stream));
-  return check_launch(fn);
+  return dispatch_prefill<true>(fn, D, vec, rows_max, p, static_cast<hipStream_t>(stream));
 }
