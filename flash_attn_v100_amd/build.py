@@ -34,6 +34,9 @@ HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # Keep the compiler from forming packed-fp32 VALU ops (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs: without it the compiler parks them in
+    # AGPRs and copies them back and forth around every branch of the kernels.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
 ]
 

@@ -24,8 +24,10 @@
 // Online softmax with lazy rescaling: the max used for the exponentials is only
 // refreshed when a tile's max exceeds it by 2^8 (wave-uniform test), so the O
 // accumulators are rarely touched outside the MFMAs.  Only tiles that cross
-// the causal diagonal or the sequence end run the masked variant; each wave
-// stops at its own diagonal.  Work items are ordered heaviest first across the
+// the causal diagonal or the sequence end apply the mask (a wave-uniform
+// branch around the mask step alone, so the MFMA code exists once and the
+// accumulators never move between register files); each wave stops at its
+// own diagonal.  Work items are ordered heaviest first across the
 // whole grid (all (batch, head) pairs of the last query tile, then the next).
 // For D <= 128 the next tile's K/V global loads are issued before the current
 // tile's MFMAs.
@@ -63,11 +65,6 @@ struct PrefillShape {
 };
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
-
-template <bool B>
-struct MaskedTag {
-  static constexpr bool value = B;
-};
 
 // Four fp16 values of V for the PV A operand: keys base..base+3 of column
 // col0 + (lane % 16), via the transposing LDS read (see the file comment).
@@ -193,8 +190,7 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
   }
   const float c = p.scale_log2;
 
-  auto compute_tile = [&](const int kt, auto masked_tag) {
-    constexpr bool MASKED = decltype(masked_tag)::value;
+  auto compute_tile = [&](const int kt, const bool masked) {
     // ---- S^T = K Q^T ----
     float16_t sacc[NBLK][RB];
 #pragma unroll
@@ -217,7 +213,7 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
     half8_t pf[RB][2 * NBLK];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      if constexpr (MASKED) {
+      if (masked) {  // uniform: only tiles crossing the diagonal or the sequence end
         const int qrow = wq0 + 32 * rb + l32;
 #pragma unroll
         for (int blk = 0; blk < NBLK; ++blk)
@@ -290,9 +286,7 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
     __syncthreads();
     if (kPrefetch && t + 1 < ntiles) fetch(kt + kBK);
     if (kt >= kend_w) continue;  // past this wave's diagonal (still joins the barriers)
-    const bool need_mask = (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > wq0);
-    if (need_mask) compute_tile(kt, MaskedTag<true>{});
-    else compute_tile(kt, MaskedTag<false>{});
+    compute_tile(kt, (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > wq0));
   }
 
   // ---- finalize and store O[qrow][d] ----
