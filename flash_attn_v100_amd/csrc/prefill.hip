@@ -1,14 +1,18 @@
 // MFMA-tiled online-softmax prefill for gfx950 (dense MHA/GQA and packed varlen).
 //
-// Workgroup = 4 waves; each wave owns RW = 64 query rows (32 when D > 128) of one
+// Workgroup = 4 waves; each wave owns RW = 64 query rows (D <= 64) or 32 of one
 // (batch, head), so a workgroup covers 4*RW rows.  The KV sequence is walked in
-// BK-key tiles (64 keys for D <= 64, 32 above, for the register budget) staged
-// in LDS, both row-major:
-//   sK [BK][DP + 8]    read (16 B per lane) as the A operand of S^T = K Q^T
-//   sV [BK][DP + 32]   read with ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T
-// Both products use v_mfma_f32_32x32x16_f16, and each K / V operand read from LDS
-// feeds RB = RW/32 MFMAs (one per 32-row query block), halving LDS traffic per
-// FLOP against one block per wave.
+// BK-key tiles (64 keys for D <= 64, 32 above) that stream through a ring of NS
+// LDS stages (3, or 2 for D > 128).  Each stage holds one K and one V tile,
+// unpadded, with the 16-byte chunks of row r XOR-swizzled by chunk_swizzle(r)
+// so that both LDS read patterns below are free of bank conflicts:
+//   K   read 16 B per lane as the A operand of S^T = K Q^T
+//   V   read with ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T
+// Tiles are copied HBM -> LDS by global_load_lds_dwordx4 (no VGPR staging), NS-1
+// tiles ahead of the one being computed, with one barrier per tile; every
+// wave waits (vmcnt) only for its own copies of the current tile.  Shapes the
+// DMA cannot serve (D not 64/128/256 or unaligned rows) stage through registers
+// into the same layout.
 //
 // S^T = K Q^T puts one query row per lane (lane l owns query l%32 of each block
 // and 16 keys of each 32-key block): the row max needs one exchange (lanes l,
@@ -17,20 +21,16 @@
 // inside each 16-key slice lane half h holds keys {4h..4h+3, 8+4h..8+4h+3}, and
 // the transposing LDS read delivers V in exactly that key order (one read per
 // 4-key run: 16 source lanes read a 4-key x 16-column block of row-major V and
-// lane i receives the 4 keys of column i).  The V row pitch is 64 bytes past a
-// multiple of 256, which makes those reads, and the 16-byte row writes, free of
-// bank conflicts.
+// lane i receives the 4 keys of column i).
 //
 // Online softmax with lazy rescaling: the max used for the exponentials is only
 // refreshed when a tile's max exceeds it by 2^8 (wave-uniform test), so the O
 // accumulators are rarely touched outside the MFMAs.  Only tiles that cross
 // the causal diagonal or the sequence end apply the mask (a wave-uniform
-// branch around the mask step alone, so the MFMA code exists once and the
-// accumulators never move between register files); each wave stops at its
-// own diagonal.  Work items are ordered heaviest first across the
-// whole grid (all (batch, head) pairs of the last query tile, then the next).
-// For D <= 128 the next tile's K/V global loads are issued before the current
-// tile's MFMAs.
+// branch around the mask step alone); each wave stops computing at its own
+// diagonal but keeps copying its share of later tiles.  Work items are ordered
+// heaviest first across the whole grid (all (batch, head) pairs of the last
+// query tile, then the next).
 #include <math.h>
 
 #include "capi_internal.h"
@@ -40,8 +40,6 @@ namespace fa {
 
 constexpr int kPreWaves = 4;
 constexpr int kPreThreads = kPreWaves * 64;
-constexpr int kKPad = 8;    // halves of padding per sK row
-constexpr int kVPad = 32;   // halves of padding per sV row (pitch = 64 B mod 256 B)
 
 struct PrefillParams {
   const half_t* q;
@@ -58,42 +56,87 @@ struct PrefillParams {
 
 template <int DP>
 struct PrefillShape {
-  static constexpr int RB = DP <= 64 ? 2 : 1;   // 32-row query blocks per wave
-  static constexpr int RW = 32 * RB;            // query rows per wave
-  static constexpr int BQ = kPreWaves * RW;     // query rows per workgroup
-  static constexpr int BK = DP <= 128 ? 64 : 32;  // keys per tile (register budget)
+  static constexpr int RB = DP <= 64 ? 2 : 1;    // 32-row query blocks per wave
+  static constexpr int RW = 32 * RB;             // query rows per wave
+  static constexpr int BQ = kPreWaves * RW;      // query rows per workgroup
+  static constexpr int BK = DP <= 64 ? 64 : 32;  // keys per tile
+  static constexpr int NS = DP <= 128 ? 3 : 2;   // LDS ring stages
+  static constexpr int TILE = BK * DP;           // halves per K (or V) tile
+  static constexpr int WAVES_PER_SIMD = DP == 128 ? 3 : (DP <= 64 ? 2 : 1);  // register budget target
 };
+
+// Physical 16-byte chunk of logical chunk c in tile row r is c ^ chunk_swizzle(r).
+// K reads: 16 lanes read rows 0..15 at one logical chunk -> 16 distinct bank
+// groups.  V transposing reads: 32 lanes read rows 4k..4k+3 at 4 consecutive
+// chunks -> 16 distinct bank groups (rows are 128 B apart for D = 64, so there
+// the row parity also selects the half of the 256-byte bank window).
+template <int DP>
+__device__ __forceinline__ int chunk_swizzle(int r) {
+  if constexpr (DP <= 64)
+    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  else
+    return ((r & 3) << 2) | ((r >> 2) & 3);
+}
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
-// Four fp16 values of V for the PV A operand: keys base..base+3 of column
-// col0 + (lane % 16), via the transposing LDS read (see the file comment).
-__device__ __forceinline__ half4_t read_v_tr(const half_t* sV, int pitch, int key_base, int col0, int lane) {
-  const int s = lane & 15;
-  const half_t* src = sV + (key_base + (s >> 2)) * pitch + col0 + 4 * (s & 3);
-  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) short4_t*)(__builtin_amdgcn_readfirstlane(0) + src));
-  return __builtin_bit_cast(half4_t, v);
+// s_waitcnt vmcnt(N) lgkmcnt(0).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
+}
+
+// One 16-byte-per-lane copy HBM -> LDS (global_load_lds_dwordx4, scalar base +
+// 32-bit lane byte offset): lane i's 16 bytes land at LDS byte address
+// lds_addr + 16 i.  Issued from asm so that the compiler does not track the
+// copy (it would otherwise wait for every copy in flight before the
+// transposing LDS reads); the caller waits with vmcnt before a barrier.  M0,
+// which holds the LDS address, is restored afterwards.
+__device__ __forceinline__ void copy16_to_lds(const half_t* base, unsigned lane_off, unsigned lds_addr) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(lane_off), "s"(base)
+      : "memory");
+}
+
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(3))) T* lds_at(unsigned byte_addr) {
+  return reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<size_t>(byte_addr));
+}
+
+// Workgroup barrier that neither waits for outstanding LDS DMA nor lets the
+// compiler move memory operations across it (the caller waits explicitly).
+__device__ __forceinline__ void tile_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <int DP, bool VARLEN, bool VEC>
-__global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kPreThreads)
+__attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void prefill_kernel(PrefillParams p) {
   using Shape = PrefillShape<DP>;
   constexpr int RB = Shape::RB;
   constexpr int RW = Shape::RW;
   constexpr int BQ = Shape::BQ;
   constexpr int kBK = Shape::BK;
+  constexpr int NS = Shape::NS;
+  constexpr int TILE = Shape::TILE;
   constexpr int NBLK = kBK / 32;              // 32-key blocks per tile
   constexpr int KK = DP / 16;                 // 16-wide d slices of QK^T
   constexpr int DB = DP / 32;                 // 32-row d blocks of PV
   constexpr int CPR = DP / 8;                 // 16-byte chunks per row
-  constexpr int RPT = kBK * CPR / kPreThreads;  // 16-byte chunks per thread per tile
-  constexpr int KP = DP + kKPad;
-  constexpr int VP = DP + kVPad;
+  constexpr int IPW = TILE / 8 / 64 / kPreWaves;  // 16-byte copies per lane per tensor per tile
   constexpr float kRescaleSlack = 8.0f;
+  static_assert(IPW * 8 * 64 * kPreWaves == TILE, "tile must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(16))) half_t sK[PrefillShape<DP>::BK * KP];
-  __shared__ __attribute__((aligned(16))) half_t sV[PrefillShape<DP>::BK * VP];
+  __shared__ __attribute__((aligned(1024))) half_t smem[NS * 2 * PrefillShape<DP>::TILE];
 
   const int D = p.D;
   // Heaviest work first: all (batch, head) pairs of the last query tile, then the next.
@@ -128,7 +171,7 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
   const int wq0 = q0 + wave * RW;  // first query row of this wave
@@ -136,6 +179,50 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
   const half_t* __restrict__ qp = p.q + q_base;
   const half_t* __restrict__ kp = p.k + k_base;
   const half_t* __restrict__ vp = p.v + k_base;
+
+  // key ranges: the workgroup walks to its last wave's diagonal, each wave stops at its own
+  const int kend_wg = p.causal ? min(seq_len, q0 + BQ) : seq_len;
+  const int kend_w = p.causal ? min(seq_len, wq0 + RW) : seq_len;
+  const int ntiles = (kend_wg + kBK - 1) / kBK;
+
+  // ---- tile copies: slot g = (wave*IPW + i)*64 + lane of a tile holds logical
+  //      chunk (g % CPR) ^ swizzle(row) of row g / CPR ----
+  const unsigned lds_base = static_cast<unsigned>(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) half_t*)smem));
+  constexpr unsigned kStageBytes = 2 * TILE * sizeof(half_t);
+  constexpr unsigned kTileBytes = TILE * sizeof(half_t);
+  int cp_row[IPW], cp_col[IPW];
+  unsigned cp_off[IPW];  // byte offset of the lane's chunk from the tile's first row
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int g = (wave * IPW + i) * 64 + lane;
+    cp_row[i] = g / CPR;
+    cp_col[i] = ((g % CPR) ^ chunk_swizzle<DP>(g / CPR)) * 8;
+    cp_off[i] = static_cast<unsigned>((cp_row[i] * stride + cp_col[i]) * sizeof(half_t));
+  }
+  auto issue = [&](int t) {
+    const int kt = t * kBK;
+    const unsigned sk = lds_base + (t % NS) * kStageBytes;
+    const half_t* kb = kp + static_cast<size_t>(kt) * stride;
+    const half_t* vb = vp + static_cast<size_t>(kt) * stride;
+    const bool tail = kt + kBK > seq_len;  // rows past the sequence end re-read its last row
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int row = tail ? min(cp_row[i], seq_len - 1 - kt) : cp_row[i];
+      const unsigned slot = sk + (wave * IPW + i) * 1024;
+      if constexpr (VEC) {
+        const unsigned off = tail ? static_cast<unsigned>((row * stride + cp_col[i]) * sizeof(half_t)) : cp_off[i];
+        copy16_to_lds(kb, off, slot);
+        copy16_to_lds(vb, off, slot + kTileBytes);
+      } else {
+        const u32x4 kx = load_row8<false>(kb + static_cast<size_t>(row) * stride, cp_col[i], D);
+        const u32x4 vx = load_row8<false>(vb + static_cast<size_t>(row) * stride, cp_col[i], D);
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(static_cast<size_t>(slot + lane * 16)) = kx;
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(static_cast<size_t>(slot + kTileBytes + lane * 16)) = vx;
+      }
+    }
+  };
+  if (ntiles > 0) issue(0);
+  if (NS > 2 && ntiles > 1) issue(1);
 
   // ---- Q fragments: B operand of S^T; block rb, lane row wq0 + 32 rb + l32, d = 16 kk + 8 hi .. +8 ----
   half8_t qf[RB][KK];
@@ -150,30 +237,6 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
       qf[rb][kk] = __builtin_bit_cast(half8_t, x);
     }
   }
-
-  // key ranges: the workgroup walks to its last wave's diagonal, each wave stops at its own
-  const int kend_wg = p.causal ? min(seq_len, q0 + BQ) : seq_len;
-  const int kend_w = p.causal ? min(seq_len, wq0 + RW) : seq_len;
-  const int ntiles = (kend_wg + kBK - 1) / kBK;
-
-  // staging: thread owns 16-byte chunk (tid % CPR) of rows (tid / CPR) + r * (256 / CPR)
-  constexpr int RSTEP = kPreThreads / CPR;
-  const int sc = tid % CPR;
-  const int srow = tid / CPR;
-  u32x4 kreg[RPT], vreg[RPT];
-  auto fetch = [&](int kt) {
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-      const int key = kt + srow + r * RSTEP;
-      const int kc = min(key, seq_len - 1);
-      kreg[r] = load_row8<VEC>(kp + static_cast<size_t>(kc) * stride, sc * 8, D);
-      vreg[r] = load_row8<VEC>(vp + static_cast<size_t>(kc) * stride, sc * 8, D);
-      if (key >= seq_len) {
-        kreg[r] = u32x4{0u, 0u, 0u, 0u};
-        vreg[r] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
 
   float16_t oacc[DB][RB];
 #pragma unroll
@@ -190,7 +253,23 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
   }
   const float c = p.scale_log2;
 
-  auto compute_tile = [&](const int kt, const bool masked) {
+  // Per-lane LDS read byte offsets with the swizzle folded in; the
+  // compile-time part of each chunk index is XORed in per read (the stage
+  // base has no bits in the chunk field).
+  //   K: row l32 (+32 blk), logical chunk 2 kk + hi.
+  const unsigned k_lane = (l32 * DP + ((chunk_swizzle<DP>(l32) ^ hi) * 8)) * sizeof(half_t);
+  //   V: source lane s = lane % 16 reads row 16 i + 8 j + 4 hi + s/4, columns
+  //   32 db + 16 ((lane >> 4) & 1) + 4 (s & 3) .. +4.
+  const int s16 = lane & 15;
+  const int v_row = 4 * hi + (s16 >> 2);
+  const int v_sw = (DP <= 64 ? ((((s16 >> 2) >> 1) & 1) << 2) : ((s16 >> 2) << 2)) | hi;
+  const unsigned v_lane =
+      (v_row * DP + (((2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1)) ^ v_sw) * 8) + (s16 & 1) * 4) * sizeof(half_t);
+
+  auto compute_tile = [&](const int t, const bool masked) {
+    const int kt = t * kBK;
+    const unsigned kaddr = lds_base + (t % NS) * kStageBytes + k_lane;
+    const unsigned vaddr = lds_base + (t % NS) * kStageBytes + kTileBytes + v_lane;
     // ---- S^T = K Q^T ----
     float16_t sacc[NBLK][RB];
 #pragma unroll
@@ -203,7 +282,7 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
     for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
       for (int blk = 0; blk < NBLK; ++blk) {
-        const half8_t a = *reinterpret_cast<const half8_t*>(&sK[(blk * 32 + l32) * KP + kk * 16 + 8 * hi]);
+        const half8_t a = *lds_at<half8_t>((kaddr ^ (32 * kk)) + blk * 32 * DP * 2);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
           sacc[blk][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[rb][kk], sacc[blk][rb], 0, 0, 0);
@@ -256,12 +335,17 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
-      const int col0 = db * 32 + 16 * ((lane >> 4) & 1);
 #pragma unroll
       for (int i = 0; i < 2 * NBLK; ++i) {
-        const half4_t lo = read_v_tr(sV, VP, 16 * i + 4 * hi, col0, lane);
-        const half4_t hi4 = read_v_tr(sV, VP, 16 * i + 8 + 4 * hi, col0, lane);
-        const half8_t a = __builtin_shufflevector(lo, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
+        half4_t part[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const unsigned src = (vaddr ^ (16 * (4 * db ^ 2 * j))) + (16 * i + 8 * j) * DP * 2;
+          const short4_t x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              const_cast<__attribute__((address_space(3))) short4_t*>(lds_at<short4_t>(src)));
+          part[j] = __builtin_bit_cast(half4_t, x);
+        }
+        const half8_t a = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
           oacc[db][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[rb][i], oacc[db][rb], 0, 0, 0);
@@ -269,24 +353,17 @@ __global__ __launch_bounds__(kPreThreads) void prefill_kernel(PrefillParams p) {
     }
   };
 
-  // D > 128 has no registers to spare for a prefetched tile: it loads each tile
-  // at the top of its own iteration instead.
-  constexpr bool kPrefetch = DP <= 128;
-  if (kPrefetch && ntiles > 0) fetch(0);
   for (int t = 0; t < ntiles; ++t) {
+    // this wave's copies of tile t have landed (tile t+1 may still be in flight)
+    if (VEC && NS > 2 && t + 1 < ntiles)
+      wait_vm_lgkm0<2 * IPW>();
+    else
+      wait_vm_lgkm0<0>();
+    tile_barrier();  // every wave's copies of tile t landed; stage (t-1) % NS is free
+    if (t + NS - 1 < ntiles) issue(t + NS - 1);
     const int kt = t * kBK;
-    if (!kPrefetch) fetch(kt);
-    __syncthreads();  // previous tile's LDS reads are done
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-      const int row = srow + r * RSTEP;
-      *reinterpret_cast<u32x4*>(&sK[row * KP + sc * 8]) = kreg[r];
-      *reinterpret_cast<u32x4*>(&sV[row * VP + sc * 8]) = vreg[r];
-    }
-    __syncthreads();
-    if (kPrefetch && t + 1 < ntiles) fetch(kt + kBK);
-    if (kt >= kend_w) continue;  // past this wave's diagonal (still joins the barriers)
-    compute_tile(kt, (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > wq0));
+    if (kt >= kend_w) continue;  // past this wave's diagonal (still copies and joins the barriers)
+    compute_tile(t, (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > wq0));
   }
 
   // ---- finalize and store O[qrow][d] ----
