@@ -1,11 +1,11 @@
 // MFMA-tiled online-softmax prefill for gfx950 (dense MHA/GQA and packed varlen).
 //
-// Workgroup = 4 waves; each wave owns RW = 64 query rows (D <= 64) or 32 of one
-// (batch, head), so a workgroup covers 4*RW rows.  The KV sequence is walked in
-// BK-key tiles (64 keys for D <= 64, 32 above) that stream through a ring of NS
-// LDS stages (3, or 2 for D > 128).  Each stage holds one K and one V tile,
-// unpadded, with the 16-byte chunks of row r XOR-swizzled by chunk_swizzle(r)
-// so that both LDS read patterns below are free of bank conflicts:
+// Workgroup = 4 waves; each wave owns RW = 32 query rows of one (batch, head),
+// so a workgroup covers 128 rows.  The KV sequence is walked in 32-key tiles
+// that stream through a ring of NS LDS stages (3, or 2 for D > 128).  Each
+// stage holds one K and one V tile, unpadded, with the 16-byte chunks of row r
+// XOR-swizzled by chunk_swizzle(r) so that both LDS read patterns below are
+// free of bank conflicts:
 //   K   read 16 B per lane as the A operand of S^T = K Q^T
 //   V   read with ds_read_b64_tr_b16 as the A operand of O^T = V^T P^T
 // Tiles are copied HBM -> LDS by global_load_lds_dwordx4 (no VGPR staging), NS-1
@@ -23,14 +23,16 @@
 // 4-key run: 16 source lanes read a 4-key x 16-column block of row-major V and
 // lane i receives the 4 keys of column i).
 //
-// Online softmax with lazy rescaling: the max used for the exponentials is only
-// refreshed when a tile's max exceeds it by 2^8 (wave-uniform test), so the O
-// accumulators are rarely touched outside the MFMAs.  Only tiles that cross
-// the causal diagonal or the sequence end apply the mask (a wave-uniform
-// branch around the mask step alone); each wave stops computing at its own
-// diagonal but keeps copying its share of later tiles.  Work items are ordered
-// heaviest first across the whole grid (all (batch, head) pairs of the last
-// query tile, then the next).
+// Online softmax with lazy rescaling: the exponentials use the running max,
+// which is only refreshed (and O, l rescaled) when some p of a tile would
+// exceed 2^8, detected from the lane's partial sum (wave-uniform test), so the
+// row max is rarely computed and the O accumulators rarely touched outside the
+// MFMAs.  Only tiles that cross the causal diagonal or the sequence end apply
+// the mask (a wave-uniform branch around the mask step alone); each wave stops
+// computing at its own diagonal but keeps copying its share of later tiles.
+// Work items are ordered heaviest first across the whole grid (all (batch,
+// head) pairs of the last query tile, then the next), which the hardware
+// dispatcher then packs onto free CUs.
 #include <math.h>
 
 #include "capi_internal.h"
@@ -54,15 +56,32 @@ struct PrefillParams {
   float scale_log2;           // (1/sqrt(D)) * log2(e)
 };
 
+// Tile shape per padded head dim.  The FA_PRE_* macros are tuning hooks for
+// building variants; the defaults are the shipped configuration.
+#ifndef FA_PRE_RB64
+#define FA_PRE_RB64 1
+#endif
+#ifndef FA_PRE_BK64
+#define FA_PRE_BK64 32
+#endif
+#ifndef FA_PRE_W64
+#define FA_PRE_W64 4
+#endif
+#ifndef FA_PRE_NS128
+#define FA_PRE_NS128 3
+#endif
+#ifndef FA_PRE_W128
+#define FA_PRE_W128 3
+#endif
 template <int DP>
 struct PrefillShape {
-  static constexpr int RB = DP <= 64 ? 2 : 1;    // 32-row query blocks per wave
-  static constexpr int RW = 32 * RB;             // query rows per wave
-  static constexpr int BQ = kPreWaves * RW;      // query rows per workgroup
-  static constexpr int BK = DP <= 64 ? 64 : 32;  // keys per tile
-  static constexpr int NS = DP <= 128 ? 3 : 2;   // LDS ring stages
-  static constexpr int TILE = BK * DP;           // halves per K (or V) tile
-  static constexpr int WAVES_PER_SIMD = DP == 128 ? 3 : (DP <= 64 ? 2 : 1);  // register budget target
+  static constexpr int RB = DP <= 64 ? FA_PRE_RB64 : 1;                 // 32-row query blocks per wave
+  static constexpr int RW = 32 * RB;                                    // query rows per wave
+  static constexpr int BQ = kPreWaves * RW;                             // query rows per workgroup
+  static constexpr int BK = DP <= 64 ? FA_PRE_BK64 : 32;                // keys per tile
+  static constexpr int NS = DP <= 64 ? 3 : (DP <= 128 ? FA_PRE_NS128 : 2);  // LDS ring stages
+  static constexpr int TILE = BK * DP;                                  // halves per K (or V) tile
+  static constexpr int WAVES_PER_SIMD = DP <= 64 ? FA_PRE_W64 : (DP <= 128 ? FA_PRE_W128 : 2);  // register budget target
 };
 
 // Physical 16-byte chunk of logical chunk c in tile row r is c ^ chunk_swizzle(r).
@@ -133,7 +152,7 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
   constexpr int DB = DP / 32;                 // 32-row d blocks of PV
   constexpr int CPR = DP / 8;                 // 16-byte chunks per row
   constexpr int IPW = TILE / 8 / 64 / kPreWaves;  // 16-byte copies per lane per tensor per tile
-  constexpr float kRescaleSlack = 8.0f;
+  constexpr float kRescaleLimit = 256.0f;  // 2^8: largest p before the max is refreshed
   static_assert(IPW * 8 * 64 * kPreWaves == TILE, "tile must split evenly over the waves");
 
   __shared__ __attribute__((aligned(1024))) half_t smem[NS * 2 * PrefillShape<DP>::TILE];
@@ -303,13 +322,31 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
             sacc[blk][rb][r] = dead ? -INFINITY : sacc[blk][rb][r];
           }
       }
-      float mx = sacc[0][rb][0];
+      // p = exp2(s c - m) against the running max m.  A lane's partial sum can
+      // only exceed 2^slack if one of its p did, i.e. some score outgrew m by
+      // more than the slack (always the case on the first tile, m = -1e30):
+      // only then is the tile's row max taken, m raised and O, l rescaled.
+      auto exponentiate = [&](float mneg) {
+        float ls = 0.0f;
 #pragma unroll
-      for (int blk = 0; blk < NBLK; ++blk)
+        for (int i = 0; i < 2 * NBLK; ++i) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[blk][rb][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
-      if (__builtin_amdgcn_ballot_w64(mx > m_run[rb] + kRescaleSlack) != 0) {
+          for (int j = 0; j < 8; ++j) {
+            const float e = fast_exp2(fmaf(sacc[i >> 1][rb][8 * (i & 1) + j], c, mneg));
+            ls += e;
+            pf[rb][i][j] = static_cast<half_t>(e);
+          }
+        }
+        return ls;
+      };
+      float ls = exponentiate(-m_run[rb]);
+      if (__builtin_amdgcn_ballot_w64(ls > kRescaleLimit) != 0) {
+        float mx = sacc[0][rb][0];
+#pragma unroll
+        for (int blk = 0; blk < NBLK; ++blk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sacc[blk][rb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
         const float mn = fmaxf(m_run[rb], mx);
         const float alpha = fast_exp2(m_run[rb] - mn);
         m_run[rb] = mn;
@@ -318,17 +355,7 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
         for (int db = 0; db < DB; ++db)
 #pragma unroll
           for (int r = 0; r < 16; ++r) oacc[db][rb][r] *= alpha;
-      }
-      const float mneg = -m_run[rb];
-      float ls = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 2 * NBLK; ++i) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e = fast_exp2(fmaf(sacc[i >> 1][rb][8 * (i & 1) + j], c, mneg));
-          ls += e;
-          pf[rb][i][j] = static_cast<half_t>(e);
-        }
+        ls = exponentiate(-mn);
       }
       l_run[rb] += ls;
     }
