@@ -131,11 +131,15 @@ __device__ __forceinline__ void wait_vmem_stores() {
 // VEC: the caller guarantees col + 8 <= d and a 16-byte aligned address, so one
 // unconditional dwordx4 load serves (the kernels use it when d equals their
 // padded width and every base pointer is 16-byte aligned).
-template <bool VEC>
+// NT: nontemporal (streaming) load, for data read exactly once.
+template <bool VEC, bool NT = false>
 __device__ __forceinline__ u32x4 load_row8(const half_t* row, int col, int d) {
   if constexpr (VEC) {
     (void)d;
-    return *reinterpret_cast<const u32x4*>(row + col);
+    if constexpr (NT)
+      return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + col));
+    else
+      return *reinterpret_cast<const u32x4*>(row + col);
   } else {
     half8_t h;
 #pragma unroll

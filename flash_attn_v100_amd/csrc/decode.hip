@@ -39,14 +39,14 @@ constexpr int kPage = 16;             // PAGE_BLOCK_SIZE of the paged cache
 #define FA_DEC_TARGET_BLOCKS 8192
 #endif
 #ifndef FA_DEC_CHUNK_QUANTUM
-#define FA_DEC_CHUNK_QUANTUM 128
+#define FA_DEC_CHUNK_QUANTUM 256
 #endif
 constexpr int kMaxChunk = 8192;                        // keys per split, upper bound
 constexpr int kChunkQuantum = FA_DEC_CHUNK_QUANTUM;    // split boundaries are multiples of this
 constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many split workgroups
 // The paged kernel stages each split's page ids in LDS before its first load,
 // one extra memory round trip per split, so it prefers fewer, longer splits.
-constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / 4;
+constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / 8;
 constexpr int kMaxSplits = 128;       // splits per sequence, upper bound
 
 struct DecodeParams {
@@ -239,6 +239,9 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   __shared__ float s_alpha[kDecWaves][GP];
   const int klast = k1 - 1;
 
+  // Continuous batching streams K/V with nontemporal loads (measured faster
+  // there; slower for the paged gathers and the INT8 path).
+  constexpr bool kStreamKV = MODE == kModeCB;
   // One iteration's K (MFMA layout) and V (row layout) registers.
   struct Tile {
     u32x4 k[T16][NC];
@@ -266,12 +269,12 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
       for (int tt = 0; tt < T16; ++tt) {
         const int t = min(t0 + 16 * tt + l16, klast);
 #pragma unroll
-        for (int c = 0; c < NC; ++c) T.k[tt][c] = load_row8<VEC>(kh + t * D, 32 * c + 8 * q4, D);
+        for (int c = 0; c < NC; ++c) T.k[tt][c] = load_row8<VEC, kStreamKV>(kh + t * D, 32 * c + 8 * q4, D);
       }
 #pragma unroll
       for (int u = 0; u < UV; ++u) {
         const int t = min(t0 + u * RPW + rg, klast);
-        T.v[u] = load_row8<VEC>(vh + t * D, col, D);
+        T.v[u] = load_row8<VEC, kStreamKV>(vh + t * D, col, D);
       }
     }
   };
