@@ -56,9 +56,18 @@ def time_gpu(fn, steps, warmup):
     """Average ms per call of fn(i), timed with HIP events on the current stream."""
     import torch
 
-    for i in range(warmup):
+    # Untimed warmup: at least `warmup` calls and at least ~0.2 s of GPU work, so
+    # the timed calls run at steady clocks (a cold GPU runs the first few
+    # hundred microseconds of work measurably slower).
+    t_end = time.perf_counter() + 0.2
+    i = 0
+    while i < warmup or time.perf_counter() < t_end:
         fn(i)
+        i += 1
+        if i % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+    warmup = i
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(st)

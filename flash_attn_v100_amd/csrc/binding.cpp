@@ -482,7 +482,7 @@ at::Tensor forward_varlen_prefill_fp16(at::Tensor q, at::Tensor k, at::Tensor v,
   TORCH_CHECK(max_seqlen > 0, "max_seqlen must be positive");
   TORCH_CHECK(batch_size > 0, "cu_seqlens must contain at least one sequence");
   HIPGuardMasqueradingAsCUDA guard(q.device());
-  auto out = at::zeros_like(q);
+  auto out = at::empty_like(q);  // the kernel zeroes every row it does not compute
   // Rows a sequence's reference grid reaches: tile*ceil(max_seqlen/tile), tile 32
   // for D <= 128 and 8 above (flash_attn_kernel.cu:3319-3320, :3336-3337).
   const int64_t tile = D <= kMaxD ? 32 : 8;

@@ -83,20 +83,29 @@ __device__ __forceinline__ int seq_len_of(const DecodeParams& p, int b) {
   }
 }
 
-// clamp(roundf(x), -127, 127) as an int; fminf/fmaxf map NaN to +127.
-__device__ __forceinline__ int quant_i8(float x) {
-  float r = __builtin_roundf(x);
-  r = fmaxf(-127.0f, fminf(127.0f, r));
-  return static_cast<int>(r);
+// Eight fp16 values -> eight int8 codes clamp(roundf(h * inv), -127, 127),
+// packed little-endian into two dwords.  Per value: clamp first (the bounds
+// are integers, so clamp-then-round equals round-then-clamp; fminf maps NaN to
+// +127), then round half away from zero as the truncating conversion of
+// c + copysign(0.5 - 2^-25, c) (exact for |c| <= 127, ties included); two
+// byte permutes and an OR pack four codes.
+__device__ __forceinline__ int quant_rh(float x) {
+  const float c = fmaxf(-127.0f, fminf(127.0f, x));
+  return static_cast<int>(c + __builtin_copysignf(0.49999997f, c));
+}
+
+__device__ __forceinline__ int pack4_i8(int a, int b, int c, int d) {
+  // perm(hi, lo, sel): selector byte k picks byte k' of lo (0-3) or of hi (4-7); 0x0c gives 0.
+  return static_cast<int>(__builtin_amdgcn_perm(b, a, 0x0c0c0400u) | __builtin_amdgcn_perm(d, c, 0x04000c0cu));
 }
 
 __device__ __forceinline__ void quant8(u32x4 raw, float inv, int& lo, int& hi) {
   half8_t h = __builtin_bit_cast(half8_t, raw);
-  int b[8];
+  int r[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) b[j] = quant_i8(static_cast<float>(h[j]) * inv) & 0xFF;
-  lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-  hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+  for (int j = 0; j < 8; ++j) r[j] = quant_rh(__builtin_fmaf(static_cast<float>(h[j]), inv, 0.0f));
+  lo = pack4_i8(r[0], r[1], r[2], r[3]);
+  hi = pack4_i8(r[4], r[5], r[6], r[7]);
 }
 
 // Per-wave LDS scratch used to hand probabilities from the MFMA layout (lane =

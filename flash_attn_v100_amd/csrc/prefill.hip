@@ -53,6 +53,7 @@ struct PrefillParams {
   int total, row_limit;       // varlen only
   int causal;
   int qtiles;                 // query tiles per (batch, head) in the grid
+  int zero_base;              // varlen only: first workgroup of the zero-fill tail
   float scale_log2;           // (1/sqrt(D)) * log2(e)
 };
 
@@ -137,6 +138,39 @@ __device__ __forceinline__ void tile_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// Varlen output rows that no sequence's attention writes are set to zero by
+// batch + 1 extra workgroups: workgroup b < batch clears rows
+// [cu[b] + min(len_b, row_limit), cu[b+1]) of sequence b, workgroup batch
+// clears [0, cu[0]) and [cu[batch], total).  Any row outside every
+// [cu[b], cu[b+1]) lies before cu[0] or at/after cu[batch] (the boundaries
+// are a path from cu[0] to cu[batch]), so every unwritten row is cleared; for
+// valid (non-decreasing) cu_seqlens the cleared rows are exactly the unwritten
+// ones and the ranges are usually empty.
+__device__ void zero_unwritten_rows(const PrefillParams& p, int z) {
+  const size_t row_halves = static_cast<size_t>(p.H_Q) * p.D;
+  auto clamp_row = [&](int r) { return max(0, min(r, p.total)); };
+  auto clear = [&](int r0, int r1) {
+    if (r0 >= r1) return;
+    half_t* base = p.o + static_cast<size_t>(r0) * row_halves;
+    const size_t n = static_cast<size_t>(r1 - r0) * row_halves;
+    if ((reinterpret_cast<uintptr_t>(base) & 15) == 0 && (n & 7) == 0) {
+      for (size_t i = threadIdx.x; i < n / 8; i += kPreThreads)
+        reinterpret_cast<u32x4*>(base)[i] = u32x4{0u, 0u, 0u, 0u};
+    } else {
+      for (size_t i = threadIdx.x; i < n; i += kPreThreads) base[i] = static_cast<half_t>(0.0f);
+    }
+  };
+  if (z < p.B) {
+    const int s = clamp_row(p.cu_seqlens[z]);
+    const int e = clamp_row(p.cu_seqlens[z + 1]);
+    const int len = e - s;
+    clear(s + max(0, min(len, p.row_limit)), e);
+  } else {
+    clear(0, clamp_row(p.cu_seqlens[0]));
+    clear(clamp_row(p.cu_seqlens[p.B]), p.total);
+  }
+}
+
 template <int DP, bool VARLEN, bool VEC>
 __global__ __launch_bounds__(kPreThreads)
 __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void prefill_kernel(PrefillParams p) {
@@ -158,6 +192,12 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
   __shared__ __attribute__((aligned(1024))) half_t smem[NS * 2 * PrefillShape<DP>::TILE];
 
   const int D = p.D;
+  if constexpr (VARLEN) {
+    if (static_cast<int>(blockIdx.x) >= p.zero_base) {
+      zero_unwritten_rows(p, static_cast<int>(blockIdx.x) - p.zero_base);
+      return;
+    }
+  }
   // Heaviest work first: all (batch, head) pairs of the last query tile, then the next.
   const int pairs = p.H_Q * p.B;
   const int qt = p.qtiles - 1 - static_cast<int>(blockIdx.x / pairs);
@@ -431,13 +471,16 @@ static void launch_prefill(bool vec, int blocks, const PrefillParams& p, hipStre
 
 static int prefill_bq(int D) { return D <= 64 ? PrefillShape<64>::BQ : (D <= 128 ? PrefillShape<128>::BQ : PrefillShape<256>::BQ); }
 
-// Launches over qtiles * H_Q * B workgroups; returns FA_OK or an error code.
+// Launches qtiles * H_Q * B attention workgroups (plus the varlen zero-fill
+// tail); returns FA_OK or an error code.
 template <bool VARLEN>
 static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, PrefillParams p, hipStream_t st) {
   p.qtiles = ceil_div(rows_max, prefill_bq(D));
-  const long long blocks = static_cast<long long>(p.qtiles) * p.H_Q * p.B;
+  const long long main_blocks = static_cast<long long>(p.qtiles) * p.H_Q * p.B;
+  const long long blocks = main_blocks + (VARLEN ? p.B + 1 : 0);
   if (blocks > 0x7fffffffLL) return set_error(FA_ERR_UNSUPPORTED, "%s: problem too large for one launch", fn);
   if (blocks == 0) return FA_OK;
+  p.zero_base = static_cast<int>(main_blocks);
   if (D <= 64) launch_prefill<64, VARLEN>(vec, static_cast<int>(blocks), p, st);
   else if (D <= 128) launch_prefill<128, VARLEN>(vec, static_cast<int>(blocks), p, st);
   else launch_prefill<256, VARLEN>(vec, static_cast<int>(blocks), p, st);
@@ -480,7 +523,7 @@ extern "C" int fa_varlen_prefill_fp16(const void* q, const void* k, const void* 
     return set_error(FA_ERR_INVALID_ARG, "%s: bad sizes (batch=%d total=%d H=%d D=%d max_seqlen=%d)", fn,
                      batch, total, H, D, max_seqlen);
   if (D > 256) return set_error(FA_ERR_UNSUPPORTED, "%s: D=%d exceeds 256", fn, D);
-  if (batch == 0 || total == 0 || row_limit == 0) return FA_OK;
+  if (batch == 0 || total == 0) return FA_OK;
   if (!q || !k || !v || !o || !cu_seqlens) return set_error(FA_ERR_INVALID_ARG, "%s: null pointer", fn);
   PrefillParams p = {};
   p.q = static_cast<const half_t*>(q);

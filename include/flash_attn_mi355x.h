@@ -57,9 +57,10 @@ int fa_prefill_fp16(const void* q, const void* k, const void* v, void* o,
 /*
  * Packed variable-length prefill.
  *   q/k/v/o [total, H, D]; cu_seqlens int32 [batch + 1] in device memory.
- *   Sequence b owns rows [cu[b], cu[b+1]); only its first `row_limit` rows are
- *   written (the reference's grid covers tile*ceil(max_seqlen/tile) rows per
- *   sequence, with tile 32 for D <= 128 and 8 above); other rows are untouched.
+ *   Sequence b owns rows [cu[b], cu[b+1]); only its first `row_limit` rows get
+ *   attention outputs (the reference's grid covers tile*ceil(max_seqlen/tile)
+ *   rows per sequence, with tile 32 for D <= 128 and 8 above); every other row
+ *   of o is set to zero, as in the reference's zero-initialised output.
  * Replaces launch_varlen_prefill_fp16_on_stream (flash_attn_kernel.cu:3302-3352)
  * behind forward_varlen_prefill_fp16 (:3354-3387) and its _stream variant
  * (:3675-3712).

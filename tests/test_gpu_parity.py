@@ -381,6 +381,22 @@ def test_varlen_prefill(fa, causal, lens, h, d, max_seqlen):
     assert_close(out, A.varlen_prefill(q, k, v, cu, ms, causal), what="varlen")
 
 
+def test_varlen_unwritten_rows_are_zero(fa):
+    """Rows outside [cu[0], cu[batch]) and past each sequence's row limit come back 0
+    (the reference returns a zero-initialised tensor), even over reused dirty memory."""
+    g = gen(77)
+    total, h, d = 100, 2, 64
+    cu = torch.tensor([3, 40, 40, 90], dtype=torch.int32)
+    q, k, v = randn(g, total, h, d), randn(g, total, h, d), randn(g, total, h, d)
+    for _ in range(2):
+        junk = torch.full((total, h, d), float("nan"), dtype=torch.float16, device=DEV)
+        del junk
+        out = fa.forward_varlen_prefill_fp16(*cuda(q, k, v, cu), 20, True)
+        ref = A.varlen_prefill(q, k, v, cu, 20, True)
+        assert_close(out, ref, what="varlen gaps")
+        assert torch.count_nonzero(out[:3]) == 0 and torch.count_nonzero(out[90:]) == 0
+
+
 def test_varlen_equals_per_sequence_prefill_and_stream(fa):
     g = gen(11)
     lens = [300, 17, 512]
