@@ -47,7 +47,8 @@ constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many spli
 // The paged kernel stages each split's page ids in LDS before its first load,
 // one extra memory round trip per split, so it prefers fewer, longer splits.
 constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / 8;
-constexpr int kMaxSplits = 128;       // splits per sequence, upper bound
+constexpr int kMaxSplits = 128;
+constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
 struct DecodeParams {
   const half_t* q;
@@ -67,6 +68,7 @@ struct DecodeParams {
   int fixed_len;               // decode / INT8: number of attended keys
   int chunk, num_splits, num_hg;
   int max_num_blocks, num_pages;
+  int lpt;                     // CB / paged: serve sequences longest first
   float scale_log2;            // (1/sqrt(D)) * log2(e)
   float scale;                 // 1/sqrt(D) (INT8 score formula)
 };
@@ -133,7 +135,6 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   const int rest = p.unit_base + slot;  // (b, h_kv, head group) unit
   const int hg = rest % p.num_hg;
   const int pair = rest / p.num_hg;
-  const int b = pair / p.H_KV;
   const int hkv = pair % p.H_KV;
   const int D = p.D;
   const int G = p.G;
@@ -141,6 +142,30 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   const int g_valid = min(GB, G - g_base);  // heads of this group that exist
 
   const int tid = threadIdx.x;
+  // Sequence served.  With per-sequence lengths (lpt set), unit rank r serves
+  // the sequence of rank r in descending length order (ties by index), so the
+  // longest sequences are dispatched first and the short ones fill the tail.
+  int b = pair / p.H_KV;
+  if constexpr (MODE == kModeCB || MODE == kModePaged) {
+    if (p.lpt) {
+      __shared__ int s_len[kLptMaxSeqs];
+      __shared__ int s_seq;
+      for (int i = tid; i < p.B; i += kDecThreads) s_len[i] = seq_len_of<MODE>(p, i);
+      __syncthreads();
+      const int r = b;
+      for (int i = tid; i < p.B; i += kDecThreads) {
+        const int li = s_len[i];
+        int rank = 0;
+        for (int j = 0; j < p.B; ++j) {
+          const int lj = s_len[j];
+          rank += (lj > li) || (lj == li && j < i);
+        }
+        if (rank == r) s_seq = i;
+      }
+      __syncthreads();
+      b = s_seq;
+    }
+  }
   const int lane = tid & 63;
   const int wave = tid >> 6;
   // MFMA layout: lane = (key l16 of a 16-key tile, quarter q)
@@ -688,6 +713,7 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   if (pl.splits > kMaxSplits)
     return set_error(FA_ERR_UNSUPPORTED, "%s: %d keys per sequence exceed %d", fn, max_len, kMaxSplits * kMaxChunk);
   p.G = p.H_Q / p.H_KV;
+  p.lpt = (MODE == kModeCB || MODE == kModePaged) && p.B > 1 && p.B <= kLptMaxSeqs;
   p.chunk = pl.chunk;
   p.num_splits = pl.splits;
   p.num_hg = pl.num_hg;

@@ -237,6 +237,21 @@ def test_continuous_batching(fa, causal, b, hq, hkv, d, max_n, cls):
     assert_close(out, A.continuous_batching(q, k, v, cl, causal), what="cb")
 
 
+@pytest.mark.parametrize("b,cls", [
+    (12, [40, 7, 40, 40, 0, 7, 90, 40, 7, 90, 3, 40]),   # ties: the longest-first order must stay a bijection
+    (600, None),                                          # more sequences than the longest-first limit (natural order)
+])
+def test_continuous_batching_ordering(fa, b, cls):
+    g = gen(12)
+    hq, hkv, d, max_n = 4, 2, 64, 96
+    if cls is None:
+        cls = torch.randint(-1, max_n, (b,), generator=g, dtype=torch.int32).tolist()
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, max_n, d), randn(g, b, hkv, max_n, d)
+    cl = torch.tensor(cls, dtype=torch.int32)
+    out = fa.forward_continuous_batching_fp16(*cuda(q, k, v, cl), True)
+    assert_close(out, A.continuous_batching(q, k, v, cl, True), what="cb order")
+
+
 def test_continuous_batching_negative_len_is_nan(fa):
     g = gen(1)
     q, k, v = randn(g, 2, 4, 1, 64), randn(g, 2, 2, 300, 64), randn(g, 2, 2, 300, 64)
