@@ -46,7 +46,10 @@ constexpr int kChunkQuantum = FA_DEC_CHUNK_QUANTUM;    // split boundaries are m
 constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many split workgroups
 // The paged kernel stages each split's page ids in LDS before its first load,
 // one extra memory round trip per split, so it prefers fewer, longer splits.
-constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / 8;
+#ifndef FA_DEC_PAGED_DIV
+#define FA_DEC_PAGED_DIV 8
+#endif
+constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / FA_DEC_PAGED_DIV;
 constexpr int kMaxSplits = 128;
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
