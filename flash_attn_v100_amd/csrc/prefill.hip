@@ -30,10 +30,14 @@
 // MFMAs.  Only tiles that cross the causal diagonal or the sequence end apply
 // the mask (a wave-uniform branch around the mask step alone); each wave stops
 // computing at its own diagonal but keeps copying its share of later tiles.
-// Work items are ordered heaviest first across the whole grid (all (batch,
-// head) pairs of the last query tile, then the next), which the hardware
-// dispatcher then packs onto free CUs.
+// Work items are dealt XCD by XCD (the dispatcher sends workgroup j to XCD
+// j % 8): each XCD owns a set of KV heads and runs them in groups of about
+// four resident rounds of workgroups, heaviest query tile first within a
+// group, so the query tiles that share K/V tiles run together behind one L2
+// and the hardware dispatcher packs the lighter ones into the tail.
 #include <math.h>
+
+#include <algorithm>
 
 #include "capi_internal.h"
 #include "common.h"
@@ -41,6 +45,14 @@
 namespace fa {
 
 constexpr int kPreWaves = 4;
+constexpr int kXcds = 8;  // XCDs per MI355X; workgroups are dealt to them round-robin
+#ifndef FA_PRE_ORDER
+#define FA_PRE_ORDER 1
+#endif
+#ifndef FA_PRE_GROUP_WGS
+#define FA_PRE_GROUP_WGS 384
+#endif
+constexpr long long kGroupWorkgroups = FA_PRE_GROUP_WGS;  // workgroups per XCD scheduling group (about 4 resident rounds)
 constexpr int kPreThreads = kPreWaves * 64;
 
 struct PrefillParams {
@@ -54,6 +66,7 @@ struct PrefillParams {
   int causal;
   int qtiles;                 // query tiles per (batch, head) in the grid
   int zero_base;              // varlen only: first workgroup of the zero-fill tail
+  int group_units;            // KV heads per XCD scheduling group
   float scale_log2;           // (1/sqrt(D)) * log2(e)
 };
 
@@ -198,6 +211,7 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
       return;
     }
   }
+#if FA_PRE_ORDER == 0
   // Heaviest work first: all (batch, head) pairs of the last query tile, then the next.
   const int pairs = p.H_Q * p.B;
   const int qt = p.qtiles - 1 - static_cast<int>(blockIdx.x / pairs);
@@ -205,6 +219,28 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
   const int h = rem % p.H_Q;
   const int b = rem / p.H_Q;
   const int hk = h / p.G;
+#else
+  // XCD-grouped order: workgroup j runs on XCD j % 8 (the dispatcher deals
+  // workgroups round-robin over the 8 XCDs), so XCD x owns the KV heads
+  // (batch, KV head) units u = x, x + 8, ...  Its stream j / 8 takes them in
+  // groups of p.group_units units and, inside a group, heaviest query tile
+  // first over all the group's (unit, query head) pairs.  A group's
+  // workgroups run together on one XCD and walk the same K/V tiles through
+  // its L2; the heaviest-first order inside the group keeps the tail short.
+  const int j = static_cast<int>(blockIdx.x);
+  const int xcd = j % kXcds;
+  const int i = j / kXcds;
+  const int heads_per_group = p.group_units * p.G;
+  const int group = i / (heads_per_group * p.qtiles);
+  const int ii = i % (heads_per_group * p.qtiles);
+  const int qt = p.qtiles - 1 - ii / heads_per_group;
+  const int hg = ii % heads_per_group;
+  const int u = xcd + kXcds * (group * p.group_units + hg / p.G);  // (batch, KV head) unit
+  if (u >= p.B * p.H_KV) return;
+  const int hk = u % p.H_KV;
+  const int b = u / p.H_KV;
+  const int h = hk * p.G + hg % p.G;
+#endif
 
   // ---- sequence geometry ----
   size_t q_base, k_base, stride;
@@ -476,7 +512,16 @@ static int prefill_bq(int D) { return D <= 64 ? PrefillShape<64>::BQ : (D <= 128
 template <bool VARLEN>
 static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, PrefillParams p, hipStream_t st) {
   p.qtiles = ceil_div(rows_max, prefill_bq(D));
+#if FA_PRE_ORDER == 0
   const long long main_blocks = static_cast<long long>(p.qtiles) * p.H_Q * p.B;
+#else
+  const long long units = static_cast<long long>(p.B) * p.H_KV;
+  const long long units_per_xcd = (units + kXcds - 1) / kXcds;
+  const long long per_unit = static_cast<long long>(p.G) * p.qtiles;
+  p.group_units = static_cast<int>(std::max<long long>(1, std::min<long long>(units_per_xcd, (kGroupWorkgroups + per_unit - 1) / per_unit)));
+  const long long groups = (units_per_xcd + p.group_units - 1) / p.group_units;
+  const long long main_blocks = groups * p.group_units * kXcds * per_unit;
+#endif
   const long long blocks = main_blocks + (VARLEN ? p.B + 1 : 0);
   if (blocks > 0x7fffffffLL) return set_error(FA_ERR_UNSUPPORTED, "%s: problem too large for one launch", fn);
   if (blocks == 0) return FA_OK;
