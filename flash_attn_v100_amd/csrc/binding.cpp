@@ -15,6 +15,7 @@
 
 #include <cmath>
 #include <unordered_map>
+#include <tuple>
 #include <vector>
 
 #include "flash_attn_mi355x.h"
@@ -515,6 +516,94 @@ void not_implemented(const char* name) {
               "forward_varlen_prefill_fp16, forward_paged_decode_gqa_fp16, forward_decode_int8_gqa)");
 }
 
+// ---------------------------------------------------------------------------
+// Host-to-device transfer helpers and the decode step that overlaps them
+
+void check_hip(hipError_t err, const char* what) {
+  TORCH_CHECK(err == hipSuccess, what, ": ", hipGetErrorString(err));
+}
+
+// async_h2d_transfer (flash_attn_kernel.cu:3714-3738)
+void async_h2d_transfer(at::Tensor dst, at::Tensor src, int64_t stream_int) {
+  TORCH_CHECK(dst.is_cuda(), "dst must be a CUDA tensor");
+  TORCH_CHECK(!src.is_cuda(), "src must be a CPU tensor");
+  TORCH_CHECK(dst.dtype() == src.dtype(), "dtype must match");
+  TORCH_CHECK(dst.numel() == src.numel(), "size must match");
+  TORCH_CHECK(src.is_pinned(), "src must be pinned memory for async transfer");
+  TORCH_CHECK(dst.is_contiguous(), "dst must be contiguous");
+  TORCH_CHECK(src.is_contiguous(), "src must be contiguous");
+  HIPGuardMasqueradingAsCUDA guard(dst.device());
+  const size_t nbytes = static_cast<size_t>(dst.numel()) * dst.element_size();
+  check_hip(hipMemcpyAsync(dst.data_ptr(), src.data_ptr(), nbytes, hipMemcpyHostToDevice,
+                           reinterpret_cast<hipStream_t>(stream_int)),
+            "async_h2d_transfer");
+}
+
+// alloc_pinned_tensor (flash_attn_kernel.cu:3740-3750): page-locked host tensor.
+at::Tensor alloc_pinned_tensor(std::vector<int64_t> sizes, int dtype_int) {
+  auto options = at::TensorOptions().dtype(static_cast<at::ScalarType>(dtype_int)).device(at::kCPU).pinned_memory(true);
+  return at::empty(sizes, options);
+}
+
+// pipeline_decode_step_out (flash_attn_kernel.cu:3786-3849): GQA decode on the
+// compute stream, then the three host-to-device copies on the transfer stream.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> pipeline_decode_step_out(
+    at::Tensor out, at::Tensor q_compute, at::Tensor k_compute, at::Tensor v_compute, at::Tensor q_transfer,
+    at::Tensor k_transfer, at::Tensor v_transfer, at::Tensor q_h2d_dst, at::Tensor k_h2d_dst, at::Tensor v_h2d_dst,
+    bool causal, int cache_len, int64_t compute_stream_int, int64_t transfer_stream_int) {
+  CHECK_INPUT(q_compute);
+  CHECK_INPUT(k_compute);
+  CHECK_INPUT(v_compute);
+  check_decode_gqa_input_shapes(q_compute, k_compute, v_compute);
+  TORCH_CHECK(q_compute.dtype() == at::kHalf, "q_compute, k_compute, v_compute must be float16");
+  TORCH_CHECK(q_compute.size(2) == 1, "q_compute sequence length must be 1 for decode mode");
+  check_decode_gqa_output_tensor(out, q_compute);
+  TORCH_CHECK(q_compute.size(3) <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  check_cache_len(cache_len, k_compute.size(2));
+  TORCH_CHECK(!q_transfer.is_cuda() && !k_transfer.is_cuda() && !v_transfer.is_cuda(),
+              "transfer source tensors must be CPU tensors");
+  TORCH_CHECK(q_transfer.is_pinned() && k_transfer.is_pinned() && v_transfer.is_pinned(),
+              "transfer source tensors must be pinned");
+  TORCH_CHECK(q_h2d_dst.is_cuda() && k_h2d_dst.is_cuda() && v_h2d_dst.is_cuda(),
+              "transfer destination tensors must be CUDA tensors");
+  TORCH_CHECK(q_transfer.dtype() == q_h2d_dst.dtype() && k_transfer.dtype() == k_h2d_dst.dtype() &&
+                  v_transfer.dtype() == v_h2d_dst.dtype(),
+              "transfer tensor dtypes must match");
+  TORCH_CHECK(q_transfer.numel() == q_h2d_dst.numel() && k_transfer.numel() == k_h2d_dst.numel() &&
+                  v_transfer.numel() == v_h2d_dst.numel(),
+              "transfer tensor sizes must match");
+  TORCH_CHECK(q_h2d_dst.device() == q_compute.device() && k_h2d_dst.device() == q_compute.device() &&
+                  v_h2d_dst.device() == q_compute.device(),
+              "transfer destinations must be on compute device");
+  TORCH_CHECK(q_compute.size(1) % k_compute.size(1) == 0, "H_Q must be divisible by H_KV");
+  HIPGuardMasqueradingAsCUDA guard(q_compute.device());
+  {
+    auto cs = c10::hip::getStreamFromExternalMasqueradingAsCUDA(reinterpret_cast<hipStream_t>(compute_stream_int),
+                                                                q_compute.device().index());
+    HIPStreamGuardMasqueradingAsCUDA sguard(cs);
+    launch_decode(q_compute, k_compute, v_compute, out, causal, cache_len);
+  }
+  if (q_transfer.numel() > 0 && q_h2d_dst.numel() > 0) {
+    hipStream_t ts = reinterpret_cast<hipStream_t>(transfer_stream_int);
+    const at::Tensor* pairs[3][2] = {{&q_h2d_dst, &q_transfer}, {&k_h2d_dst, &k_transfer}, {&v_h2d_dst, &v_transfer}};
+    for (auto& pr : pairs)
+      check_hip(hipMemcpyAsync(pr[0]->data_ptr(), pr[1]->data_ptr(),
+                               static_cast<size_t>(pr[0]->numel()) * pr[0]->element_size(), hipMemcpyHostToDevice, ts),
+                "pipeline_decode_step");
+  }
+  return std::make_tuple(out, q_h2d_dst, k_h2d_dst);
+}
+
+// pipeline_decode_step (flash_attn_kernel.cu:3752-3784)
+std::tuple<at::Tensor, at::Tensor, at::Tensor> pipeline_decode_step(
+    at::Tensor q_compute, at::Tensor k_compute, at::Tensor v_compute, at::Tensor q_transfer, at::Tensor k_transfer,
+    at::Tensor v_transfer, at::Tensor q_h2d_dst, at::Tensor k_h2d_dst, at::Tensor v_h2d_dst, bool causal,
+    int cache_len, int64_t compute_stream_int, int64_t transfer_stream_int) {
+  auto out = at::empty({q_compute.size(0), q_compute.size(1), 1, q_compute.size(3)}, q_compute.options());
+  return pipeline_decode_step_out(out, q_compute, k_compute, v_compute, q_transfer, k_transfer, v_transfer, q_h2d_dst,
+                                  k_h2d_dst, v_h2d_dst, causal, cache_len, compute_stream_int, transfer_stream_int);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -535,8 +624,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_varlen_prefill_fp16", &forward_varlen_prefill_fp16, "Packed varlen prefill (MI355X MFMA)");
   m.def("forward_varlen_prefill_fp16_stream", &forward_varlen_prefill_fp16_stream,
         "Packed varlen prefill on a given stream");
-  for (const char* name : {"forward", "forward_with_lse", "forward_fp16_with_lse", "backward", "async_h2d_transfer",
-                           "alloc_pinned_tensor", "pipeline_decode_step", "pipeline_decode_step_out",
+  m.def("async_h2d_transfer", &async_h2d_transfer, "Async host-to-device copy from pinned memory");
+  m.def("alloc_pinned_tensor", &alloc_pinned_tensor, "Allocate a pinned (page-locked) host tensor");
+  m.def("pipeline_decode_step", &pipeline_decode_step, "GQA decode on one stream, H2D copies on another");
+  m.def("pipeline_decode_step_out", &pipeline_decode_step_out,
+        "GQA decode into out on one stream, H2D copies on another");
+  for (const char* name : {"forward", "forward_with_lse", "forward_fp16_with_lse", "backward",
                            "speculative_verify", "forward_decode_int8_kv_cache_gqa", "token_eviction",
                            "forward_decode_sliding_window_gqa", "cross_gpu_allreduce_fp16", "scatter_heads",
                            "gather_heads"}) {

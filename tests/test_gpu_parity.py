@@ -485,3 +485,85 @@ def test_decode_int8_config5b_sampled(fa):
     ref = A.decode_int8(q, k, v, qs, ks, 2048)
     assert rel_l2(out, ref) <= INT8_REL_L2
     assert_close(out, ref, what="cfg5b")
+
+
+# ---------------------------------------------------------------- transfer helpers and the overlapped decode step
+
+def test_alloc_pinned_tensor(fa):
+    """test_async.py:146-164: dtype code 5 is float16, the tensor is page-locked host memory."""
+    t = fa.alloc_pinned_tensor([2, 8, 512, 64], 5)
+    assert list(t.shape) == [2, 8, 512, 64] and t.dtype == torch.float16
+    assert t.device.type == "cpu" and t.is_pinned()
+
+
+def test_async_h2d_transfer(fa):
+    """test_async.py:115-143: a pinned host tensor copied on a side stream arrives intact."""
+    g = gen(5)
+    src = fa.alloc_pinned_tensor([2, 8, 1, 64], 5)
+    src.copy_(randn(g, 2, 8, 1, 64))
+    dst = torch.empty(2, 8, 1, 64, dtype=torch.float16, device=DEV)
+    st = torch.cuda.Stream()
+    fa.async_h2d_transfer(dst, src, st.cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dst.cpu(), src)
+    with pytest.raises(RuntimeError):
+        fa.async_h2d_transfer(dst, src.clone(), st.cuda_stream)  # not pinned
+    with pytest.raises(RuntimeError):
+        fa.async_h2d_transfer(dst, src.to(DEV), st.cuda_stream)  # not a host tensor
+
+
+@pytest.mark.parametrize("use_out", [True, False])
+def test_pipeline_decode_step(fa, use_out):
+    """test_async.py:166-214: decode on the compute stream equals forward_decode_gqa_fp16, the
+    three host-to-device copies on the transfer stream land, and _out returns the caller's buffer."""
+    B, H_Q, H_KV, N, D = 2, 8, 2, 512, 64
+    g = gen(42)
+    q, k, v = randn(g, B, H_Q, 1, D), randn(g, B, H_KV, N, D), randn(g, B, H_KV, N, D)
+    qc, kc, vc = cuda(q, k, v)
+    host = [fa.alloc_pinned_tensor(list(s), 5) for s in ([B, H_Q, 1, D], [B, H_KV, N, D], [B, H_KV, N, D])]
+    for h in host:
+        h.copy_(randn(g, *h.shape))
+    dst = [torch.empty(h.shape, dtype=torch.float16, device=DEV) for h in host]
+    cs, ts = torch.cuda.Stream(), torch.cuda.Stream()
+    if use_out:
+        out_buf = torch.empty(B, H_Q, 1, D, dtype=torch.float16, device=DEV)
+        out, q_dst, k_dst = fa.pipeline_decode_step_out(out_buf, qc, kc, vc, *host, *dst, True, 0,
+                                                        cs.cuda_stream, ts.cuda_stream)
+        assert out.data_ptr() == out_buf.data_ptr()
+    else:
+        out, q_dst, k_dst = fa.pipeline_decode_step(qc, kc, vc, *host, *dst, True, 0, cs.cuda_stream, ts.cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out, fa.forward_decode_gqa_fp16(qc, kc, vc, True, 0))
+    assert_close(out, A.decode(q, k, v, True, 0), what="pipeline decode")
+    assert q_dst.data_ptr() == dst[0].data_ptr() and k_dst.data_ptr() == dst[1].data_ptr()
+    for d_, h in zip(dst, host):
+        assert torch.equal(d_.cpu(), h)
+    with pytest.raises(RuntimeError):
+        fa.pipeline_decode_step(qc, kc, vc, host[0].clone(), *host[1:], *dst, True, 0,
+                                cs.cuda_stream, ts.cuda_stream)  # unpinned source
+
+
+def test_decode_graph_capture_replays(fa):
+    """Decode calls captured in a HIP graph (no memset nodes: the split workspace already exists
+    on the capture stream) replay to the eager results, with eager work between replays."""
+    g = gen(9)
+    sets = [(randn(g, 1, 32, 1, 128), randn(g, 1, 8, 1025, 128), randn(g, 1, 8, 1025, 128)) for _ in range(3)]
+    dev = [cuda(*s) for s in sets]
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        for q, k, v in dev:
+            fa.forward_decode_gqa_fp16(q, k, v, True, 1024)
+    st.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        outs = [fa.forward_decode_gqa_fp16(q, k, v, True, 1024) for q, k, v in dev]
+    refs = [A.decode(q, k, v, True, 1024) for q, k, v in sets]
+    for _ in range(3):
+        eager = [fa.forward_decode_gqa_fp16(q, k, v, True, 1024) for q, k, v in dev]
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for o, e, r in zip(outs, eager, refs):
+            assert torch.equal(o, e)
+            assert_close(o, r, what="graph replay")
