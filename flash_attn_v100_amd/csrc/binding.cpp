@@ -516,6 +516,33 @@ void not_implemented(const char* name) {
               "forward_varlen_prefill_fp16, forward_paged_decode_gqa_fp16, forward_decode_int8_gqa)");
 }
 
+// forward_decode_sliding_window_gqa (flash_attn_kernel.cu:4484-4535): keys k < sink_size
+// plus the window [max(0, min(cache_len+1, N) - window_size), cache_len]; `causal` is unused.
+at::Tensor forward_decode_sliding_window_gqa(at::Tensor q, at::Tensor k, at::Tensor v, bool causal, int cache_len,
+                                             int window_size, int sink_size) {
+  (void)causal;
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q must be float16");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  const auto H_Q = q.size(1), H_KV = k.size(1);
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(q.size(3) <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  // The reference reads k/v without checking them; here a mismatch is an error.
+  check_decode_gqa_input_shapes(q, k, v);
+  TORCH_CHECK(k.dtype() == at::kHalf && v.dtype() == at::kHalf, "k, v must be float16");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty({q.size(0), H_Q, 1, q.size(3)}, q.options());
+  const int B = to_int(q.size(0), "B"), N = to_int(k.size(2), "N"), D = to_int(q.size(3), "D");
+  auto ws = decode_workspace(q, B, to_int(H_Q, "H_Q"), to_int(H_KV, "H_KV"), N, D);
+  check_fa(fa_decode_sliding_window_gqa(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B,
+                                        to_int(H_Q, "H_Q"), to_int(H_KV, "H_KV"), N, D, cache_len, window_size,
+                                        sink_size, ws_ptr(ws), ws_bytes(ws), cur_stream()));
+  return out;
+}
+
 // ---------------------------------------------------------------------------
 // Host-to-device transfer helpers and the decode step that overlaps them
 
@@ -624,6 +651,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_varlen_prefill_fp16", &forward_varlen_prefill_fp16, "Packed varlen prefill (MI355X MFMA)");
   m.def("forward_varlen_prefill_fp16_stream", &forward_varlen_prefill_fp16_stream,
         "Packed varlen prefill on a given stream");
+  m.def("forward_decode_sliding_window_gqa", &forward_decode_sliding_window_gqa,
+        "Sliding-window + attention-sink GQA decode (MI355X split-KV)");
   m.def("async_h2d_transfer", &async_h2d_transfer, "Async host-to-device copy from pinned memory");
   m.def("alloc_pinned_tensor", &alloc_pinned_tensor, "Allocate a pinned (page-locked) host tensor");
   m.def("pipeline_decode_step", &pipeline_decode_step, "GQA decode on one stream, H2D copies on another");
@@ -631,7 +660,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "GQA decode into out on one stream, H2D copies on another");
   for (const char* name : {"forward", "forward_with_lse", "forward_fp16_with_lse", "backward",
                            "speculative_verify", "forward_decode_int8_kv_cache_gqa", "token_eviction",
-                           "forward_decode_sliding_window_gqa", "cross_gpu_allreduce_fp16", "scatter_heads",
+                           "cross_gpu_allreduce_fp16", "scatter_heads",
                            "gather_heads"}) {
     std::string n(name);
     m.def(name, [n](pybind11::args, pybind11::kwargs) { not_implemented(n.c_str()); }, "Not implemented on MI355X");

@@ -23,6 +23,8 @@
 // replays) without any memset.
 #include <math.h>
 
+#include <algorithm>
+
 #include "capi_internal.h"
 #include "common.h"
 
@@ -72,6 +74,8 @@ struct DecodeParams {
   int chunk, num_splits, num_hg;
   int max_num_blocks, num_pages;
   int lpt;                     // CB / paged: serve sequences longest first
+  int seg1, seg_shift;         // contiguous modes: key v < seg1 is row v, later keys row v + seg_shift
+                               // (seg_shift = 0: identity; sliding window: sink run, then window run)
   float scale_log2;            // (1/sqrt(D)) * log2(e)
   float scale;                 // 1/sqrt(D) (INT8 score formula)
 };
@@ -302,15 +306,16 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     } else {
       const half_t* kh = p.k + kv_head_base;
       const half_t* vh = p.v + kv_head_base;
+      auto row_of = [&](int t) { return t < p.seg1 ? t : t + p.seg_shift; };
 #pragma unroll
       for (int tt = 0; tt < T16; ++tt) {
-        const int t = min(t0 + 16 * tt + l16, klast);
+        const int t = row_of(min(t0 + 16 * tt + l16, klast));
 #pragma unroll
         for (int c = 0; c < NC; ++c) T.k[tt][c] = load_row8<VEC, kStreamKV>(kh + t * D, 32 * c + 8 * q4, D);
       }
 #pragma unroll
       for (int u = 0; u < UV; ++u) {
-        const int t = min(t0 + u * RPW + rg, klast);
+        const int t = row_of(min(t0 + u * RPW + rg, klast));
         T.v[u] = load_row8<VEC, kStreamKV>(vh + t * D, col, D);
       }
     }
@@ -769,6 +774,35 @@ extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void*
   p.o = static_cast<half_t*>(o);
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
   p.fixed_len = causal ? cache_len + 1 : N;
+  return run_decode<kModeDecode>(fn, p, N, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fa_decode_sliding_window_gqa(const void* q, const void* k, const void* v, void* o, int B,
+                                           int H_Q, int H_KV, int N, int D, int cache_len, int window_size,
+                                           int sink_size, void* workspace, size_t workspace_bytes, void* stream) {
+  const char* fn = "fa_decode_sliding_window_gqa";
+  int rc = check_common(fn, B, H_Q, H_KV, D);
+  if (rc != FA_OK) return rc;
+  if (N <= 0) return set_error(FA_ERR_INVALID_ARG, "%s: N must be positive", fn);
+  if (B > 0 && (!q || !k || !v || !o)) return set_error(FA_ERR_INVALID_ARG, "%s: null tensor pointer", fn);
+  // Attended keys: k < sink_size (whatever cache_len is), and
+  // window_start <= k <= cache_len with window_start = max(0, min(cache_len+1, N) - window_size).
+  // As one key sequence: the sink run [0, L1), then the window run from max(window_start, L1).
+  const long long eff_end = std::min<long long>(static_cast<long long>(cache_len) + 1, N);
+  const long long wstart = std::max<long long>(0, eff_end - window_size);
+  const int L1 = static_cast<int>(std::min<long long>(std::max(sink_size, 0), N));
+  const long long lo = std::max<long long>(wstart, L1);
+  const long long hi = std::min<long long>(cache_len, static_cast<long long>(N) - 1);
+  const int L2 = hi >= lo ? static_cast<int>(hi - lo + 1) : 0;
+  DecodeParams p = {};
+  p.q = static_cast<const half_t*>(q);
+  p.k = static_cast<const half_t*>(k);
+  p.v = static_cast<const half_t*>(v);
+  p.o = static_cast<half_t*>(o);
+  p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
+  p.fixed_len = L1 + L2;
+  p.seg1 = L1;
+  p.seg_shift = static_cast<int>(lo - L1);
   return run_decode<kModeDecode>(fn, p, N, workspace, workspace_bytes, stream);
 }
 

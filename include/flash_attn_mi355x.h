@@ -91,6 +91,20 @@ int fa_decode_fp16(const void* q, const void* k, const void* v, void* o,
                    void* stream);
 
 /*
+ * Sliding-window (+ attention-sink) GQA decode against a contiguous cache.
+ *   Attends key k iff k < sink_size, or window_start <= k <= cache_len with
+ *   window_start = max(0, min(cache_len + 1, N) - window_size); no keys -> NaN.
+ *   cache_len is not range-checked (keys stay inside [0, N)).  Workspace as for
+ *   fa_decode_fp16 (max_len = N).
+ * Replaces flash_attn_kernel_decode_sliding_window_gqa (flash_attn_kernel.cu:4346-4482)
+ * behind flash_attn_forward_decode_sliding_window_gqa (:4484-4535, bound at flash_attn.cpp:251).
+ */
+int fa_decode_sliding_window_gqa(const void* q, const void* k, const void* v, void* o, int B,
+                                 int H_Q, int H_KV, int N, int D, int cache_len,
+                                 int window_size, int sink_size, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/*
  * Continuous-batching decode: per-sequence cache lengths.
  *   q/o [B, H_Q, 1, D], k/v [B, H_KV, max_N, D], cache_lens int32 [B] (device).
  *   Sequence b attends keys [0, min(cache_lens[b] + 1, max_N)); an empty range

@@ -23,8 +23,10 @@ pure-Python fp64 loop restatement (``oracle/brute.py``) on tiny inputs, against
 closed forms (cache_len=0 -> V[0], identical keys -> mean(V), a dominant key ->
 its V row), against invariants (GQA == MHA on repeat-interleaved KV, paged ==
 contiguous on the gathered cache, varlen == per-segment prefill, continuous
-batching == per-row decode on the truncated cache) and against the committed
-fixtures in ``tests/golden/``.
+batching == per-row decode on the truncated cache, a sliding window that
+covers every key == plain decode, an INT8 cache with power-of-two scales ==
+decode on the exactly dequantized cache) and against the committed fixtures in
+``tests/golden/``.
 """
 from __future__ import annotations
 
@@ -294,3 +296,50 @@ def decode_int8_dequant_reference(q, k, v, q_scale, k_scale, cache_len: int):
     qd = quantize_int8(q, qs.view(b_, h_q, 1, 1)).to(torch.float64) * qs.view(b_, h_q, 1, 1).double()
     kd = quantize_int8(k, ks.view(b_, h_kv, 1, 1)).to(torch.float64) * ks.view(b_, h_kv, 1, 1).double()
     return decode(qd, kd, v.double(), True, cache_len, compute_dtype=torch.float64)
+
+
+def sliding_window_mask(n: int, cache_len: int, window_size: int, sink_size: int) -> torch.Tensor:
+    """True where key k is masked for ``forward_decode_sliding_window_gqa``.
+
+    effective_end = min(cache_len + 1, N), window_start = max(0, effective_end -
+    window_size) (flash_attn_kernel.cu:4386-4387); key k is kept iff
+    ``k < sink_size`` or ``window_start <= k <= cache_len`` (:4413-4416).
+    """
+    k = torch.arange(n)
+    eff_end = min(cache_len + 1, n)
+    wstart = max(0, eff_end - window_size)
+    keep = (k < sink_size) | ((k >= wstart) & (k <= cache_len))
+    return ~keep
+
+
+def decode_sliding_window(q, k, v, cache_len: int, window_size: int, sink_size: int,
+                          compute_dtype=torch.float32):
+    """``forward_decode_sliding_window_gqa`` (flash_attn_kernel.cu:4346-4535).
+
+    GQA map as in decode; the ``causal`` argument is unused by the reference;
+    no attended key gives 0/0 = NaN.
+    """
+    n = k.shape[2]
+    mask = sliding_window_mask(n, cache_len, window_size, sink_size).view(1, 1, 1, n)
+    return _attend(q, expand_kv(k, q.shape[1]), expand_kv(v, q.shape[1]), mask, compute_dtype)
+
+
+def dequant_int8_cache(x_i8: torch.Tensor, scale_f16: torch.Tensor) -> torch.Tensor:
+    """INT8 KV-cache element -> fp16: ``__float2half((float)x * __half2float(scale[token]))``
+    (flash_attn_kernel.cu:4083-4086); the fp32 product of an int8 and an fp16 is exact."""
+    return (x_i8.to(torch.float32) * scale_f16.to(torch.float32).unsqueeze(-1)).to(torch.float16)
+
+
+def decode_int8_kv_cache(q, k_i8, v_i8, k_scale, v_scale, cache_len: int,
+                         compute_dtype=torch.float32):
+    """``forward_decode_int8_kv_cache_gqa`` (flash_attn_kernel.cu:4020-4221).
+
+    K/V int8 [B,H_KV,N,D] with fp16 per-token scales [B,H_KV,N], dequantized to
+    fp16 before use; keys ``k > cache_len`` are always masked (:4094, no causal
+    flag, cache_len unchecked); no attended key gives NaN.
+    """
+    n = k_i8.shape[2]
+    kd = dequant_int8_cache(k_i8, k_scale)
+    vd = dequant_int8_cache(v_i8, v_scale)
+    mask = (torch.arange(n) > cache_len).view(1, 1, 1, n)
+    return _attend(q, expand_kv(kd, q.shape[1]), expand_kv(vd, q.shape[1]), mask, compute_dtype)

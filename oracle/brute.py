@@ -15,6 +15,7 @@ use only for shapes of a few thousand elements.
 from __future__ import annotations
 
 import math
+import struct
 
 FLT_MAX = 3.4028234663852886e38
 PAGE = 16  # PAGE_BLOCK_SIZE (flash_attn_kernel.cu:3389)
@@ -219,4 +220,50 @@ def decode_int8(q, k, v, q_scale, k_scale, cache_len):
             p = [math.exp(sc[j] - m) if j <= cache_len else 0.0 for j in range(n)]
             l_ = sum(p)
             out[b][h] = [[sum(p[j] * v[b][g][j][t] for j in range(n)) / l_ for t in range(d)]]
+    return out
+
+
+def decode_sliding_window(q, k, v, cache_len, window_size, sink_size):
+    """forward_decode_sliding_window_gqa kernel (flash_attn_kernel.cu:4346-4482): keys
+    0..N-1 in tiles of 64; key j kept iff j < sink_size or window_start <= j <= cache_len,
+    window_start = max(0, min(cache_len + 1, N) - window_size) (:4386-4387, :4413-4416)."""
+    q, k, v = _tolist(q), _tolist(k), _tolist(v)
+    b_, hq, d = len(q), len(q[0]), len(q[0][0][0])
+    hkv, n = len(k[0]), len(k[0][0])
+    scale = 1.0 / math.sqrt(d)
+    eff_end = min(cache_len + 1, n)
+    wstart = max(0, eff_end - window_size)
+    out = [[None] * hq for _ in range(b_)]
+    for b in range(b_):
+        for h in range(hq):
+            g = h // (hq // hkv)
+            out[b][h] = [_online_attend(
+                q[b][h][0], k[b][g], v[b][g],
+                lambda j: not (j < sink_size or (wstart <= j <= cache_len)), scale, 64)]
+    return out
+
+
+def _to_half(x):
+    """Round to the nearest fp16 value, ties to even (IEEE binary16 packing)."""
+    return struct.unpack("<e", struct.pack("<e", x))[0]
+
+
+def decode_int8_kv_cache(q, k_i8, v_i8, k_scale, v_scale, cache_len):
+    """forward_decode_int8_kv_cache_gqa kernel (flash_attn_kernel.cu:4020-4159): each
+    element dequantized to half(x * scale[token]) in the tile load (:4083-4086), keys
+    j > cache_len masked (:4094), online softmax over tiles of 64."""
+    q, k_i8, v_i8 = _tolist(q), _tolist(k_i8), _tolist(v_i8)
+    k_scale, v_scale = _tolist(k_scale), _tolist(v_scale)
+    b_, hq, d = len(q), len(q[0]), len(q[0][0][0])
+    hkv, n = len(k_i8[0]), len(k_i8[0][0])
+    scale = 1.0 / math.sqrt(d)
+    out = [[None] * hq for _ in range(b_)]
+    for b in range(b_):
+        kd = [[[_to_half(float(k_i8[b][g][j][t]) * float(k_scale[b][g][j])) for t in range(d)]
+               for j in range(n)] for g in range(hkv)]
+        vd = [[[_to_half(float(v_i8[b][g][j][t]) * float(v_scale[b][g][j])) for t in range(d)]
+               for j in range(n)] for g in range(hkv)]
+        for h in range(hq):
+            g = h // (hq // hkv)
+            out[b][h] = [_online_attend(q[b][h][0], kd[g], vd[g], lambda j: j > cache_len, scale, 64)]
     return out

@@ -567,3 +567,35 @@ def test_decode_graph_capture_replays(fa):
         for o, e, r in zip(outs, eager, refs):
             assert torch.equal(o, e)
             assert_close(o, r, what="graph replay")
+
+
+# ---------------------------------------------------------------- sliding-window decode
+
+@pytest.mark.parametrize("b,hq,hkv,n,d,cache_len,window,sink", [
+    (2, 8, 2, 512, 64, 300, 64, 4),        # sink + window, far apart
+    (1, 32, 8, 4097, 128, 4096, 1024, 16),  # config-2-like shape, long window
+    (2, 4, 4, 300, 128, 100, 200, 150),    # sink overlaps the window
+    (1, 8, 2, 200, 64, 50, 8, 100),        # sink past cache_len (still attended)
+    (1, 4, 1, 128, 256, 127, 1000, 0),     # window covers everything
+    (1, 4, 2, 96, 80, 40, 0, 3),           # zero window: sink only, odd D
+    (2, 4, 2, 64, 64, -1, 4, 0),           # nothing attended -> NaN
+    (1, 4, 2, 64, 64, 500, 16, 2),         # cache_len >= N: window ends at N-1
+])
+def test_decode_sliding_window(fa, b, hq, hkv, n, d, cache_len, window, sink):
+    g = gen(n + d + window)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+    out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, cache_len, window, sink)
+    assert_close(out, A.decode_sliding_window(q, k, v, cache_len, window, sink), what="sliding window")
+
+
+def test_decode_sliding_window_validation(fa):
+    x = torch.zeros(1, 4, 1, 64, dtype=torch.float16, device=DEV)
+    kv = torch.zeros(1, 3, 32, 64, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_sliding_window_gqa(x, kv, kv, True, 10, 4, 0)  # H_Q % H_KV != 0
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_sliding_window_gqa(x.float(), kv, kv, True, 10, 4, 0)
+    q2 = torch.zeros(1, 4, 2, 64, dtype=torch.float16, device=DEV)
+    kv2 = torch.zeros(1, 2, 32, 64, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_sliding_window_gqa(q2, kv2, kv2, True, 10, 4, 0)  # q_len != 1

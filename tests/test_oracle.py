@@ -278,3 +278,56 @@ def test_oracle_matches_golden(fname):
     else:
         raise AssertionError(kind)
     close(out, fx["out"], tol=1e-6)
+
+
+# ---------------------------------------------------------------- next-row decode variants
+
+@pytest.mark.parametrize("cache_len,window,sink", [
+    (69, 16, 4), (69, 16, 0), (69, 200, 0), (30, 8, 40), (69, 0, 5), (5, 3, 5),
+    (100, 10, 2), (-1, 4, 0), (-1, 4, 3), (40, -3, 2), (0, 1, 0),
+])
+def test_sliding_window_vs_brute(cache_len, window, sink):
+    """Window/sink index rules (flash_attn_kernel.cu:4386-4387, :4413-4416) against the
+    kernel-loop restatement, including sinks past cache_len, windows past N, an
+    empty key set (NaN) and cache_len >= N."""
+    g = torch.Generator().manual_seed(11)
+    q, k, v = randn(g, 2, 4, 1, 8), randn(g, 2, 2, 70, 8), randn(g, 2, 2, 70, 8)
+    close(A.decode_sliding_window(q, k, v, cache_len, window, sink, F64),
+          t64(Bt.decode_sliding_window(q.double(), k.double(), v.double(), cache_len, window, sink)))
+
+
+def test_sliding_window_reductions():
+    """A window covering every key is causal decode; a sink covering every key is the
+    non-causal decode; a zero window keeps exactly the sink keys."""
+    g = torch.Generator().manual_seed(12)
+    q, k, v = randn(g, 1, 4, 1, 8), randn(g, 1, 2, 50, 8), randn(g, 1, 2, 50, 8)
+    close(A.decode_sliding_window(q, k, v, 30, 1000, 0, F64), A.decode(q, k, v, True, 30, F64))
+    close(A.decode_sliding_window(q, k, v, 30, 1, 50, F64), A.decode(q, k, v, False, 30, F64))
+    close(A.decode_sliding_window(q, k, v, 30, 0, 7, F64), A.decode(q, k[:, :, :7], v[:, :, :7], False, 0, F64))
+
+
+@pytest.mark.parametrize("cache_len", [0, 40, 69, 200, -1])
+def test_int8_kv_cache_vs_brute(cache_len):
+    """Per-token fp16-scale dequantization to half (flash_attn_kernel.cu:4083-4086) and
+    the always-on k > cache_len mask (:4094) against the kernel-loop restatement."""
+    g = torch.Generator().manual_seed(13)
+    q = randn(g, 2, 4, 1, 8)
+    k_i8 = torch.randint(-127, 128, (2, 2, 70, 8), generator=g, dtype=torch.int8)
+    v_i8 = torch.randint(-127, 128, (2, 2, 70, 8), generator=g, dtype=torch.int8)
+    ks = (torch.rand(2, 2, 70, generator=g) * 0.05 + 1e-3).half()
+    vs = (torch.rand(2, 2, 70, generator=g) * 0.05 + 1e-3).half()
+    close(A.decode_int8_kv_cache(q, k_i8, v_i8, ks, vs, cache_len, F64),
+          t64(Bt.decode_int8_kv_cache(q.double(), k_i8, v_i8, ks, vs, cache_len)))
+
+
+def test_int8_kv_cache_exact_scales_reduce_to_decode():
+    """With power-of-two scales the dequantized cache is exact, so the result is the
+    plain causal decode on int8 * scale."""
+    g = torch.Generator().manual_seed(14)
+    q = randn(g, 1, 8, 1, 16)
+    k_i8 = torch.randint(-127, 128, (1, 2, 33, 16), generator=g, dtype=torch.int8)
+    v_i8 = torch.randint(-127, 128, (1, 2, 33, 16), generator=g, dtype=torch.int8)
+    ks = torch.full((1, 2, 33), 2.0 ** -6).half()
+    vs = torch.full((1, 2, 33), 2.0 ** -5).half()
+    kd, vd = k_i8.double() * 2.0 ** -6, v_i8.double() * 2.0 ** -5
+    close(A.decode_int8_kv_cache(q, k_i8, v_i8, ks, vs, 20, F64), A.decode(q, kd, vd, True, 20, F64))
