@@ -516,6 +516,44 @@ void not_implemented(const char* name) {
               "forward_varlen_prefill_fp16, forward_paged_decode_gqa_fp16, forward_decode_int8_gqa)");
 }
 
+// forward_decode_int8_kv_cache_gqa (flash_attn_kernel.cu:4161-4221)
+at::Tensor forward_decode_int8_kv_cache_gqa(at::Tensor q, at::Tensor k_int8, at::Tensor v_int8, at::Tensor k_scale,
+                                            at::Tensor v_scale, int cache_len) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k_int8);
+  CHECK_INPUT(v_int8);
+  CHECK_INPUT(k_scale);
+  CHECK_INPUT(v_scale);
+  TORCH_CHECK(q.dtype() == at::kHalf, "q must be float16");
+  TORCH_CHECK(k_int8.dtype() == at::kChar, "k_int8 must be int8");
+  TORCH_CHECK(v_int8.dtype() == at::kChar, "v_int8 must be int8");
+  TORCH_CHECK(k_scale.dtype() == at::kHalf, "k_scale must be float16");
+  TORCH_CHECK(v_scale.dtype() == at::kHalf, "v_scale must be float16");
+  TORCH_CHECK(q.size(2) == 1, "q sequence length must be 1 for decode mode");
+  const auto B = q.size(0), H_Q = q.size(1), H_KV = k_int8.size(1), N = k_int8.size(2), D = q.size(3);
+  TORCH_CHECK(H_Q >= H_KV, "H_Q must be >= H_KV");
+  TORCH_CHECK(H_Q % H_KV == 0, "H_Q must be divisible by H_KV");
+  TORCH_CHECK(D <= kMaxDLarge, "D must be <= MAX_D_LARGE(256)");
+  TORCH_CHECK(k_int8.size(3) == D, "k_int8 last dim must match D");
+  TORCH_CHECK(v_int8.size(3) == D, "v_int8 last dim must match D");
+  TORCH_CHECK(k_scale.size(2) == N, "k_scale size mismatch");
+  TORCH_CHECK(v_scale.size(2) == N, "v_scale size mismatch");
+  // The reference reads these without checking them; here a mismatch is an error.
+  TORCH_CHECK(q.dim() == 4 && k_int8.dim() == 4 && k_int8.sizes() == v_int8.sizes() && k_int8.size(0) == B,
+              "k_int8 and v_int8 must be [B, H_KV, N, D]");
+  TORCH_CHECK(k_scale.dim() == 3 && k_scale.size(0) == B && k_scale.size(1) == H_KV && k_scale.sizes() == v_scale.sizes(),
+              "k_scale and v_scale must be [B, H_KV, N]");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty({B, H_Q, 1, D}, q.options());
+  const int b = to_int(B, "B"), hq = to_int(H_Q, "H_Q"), hkv = to_int(H_KV, "H_KV"), n = to_int(N, "N"),
+            d = to_int(D, "D");
+  auto ws = decode_workspace(q, b, hq, hkv, n, d);
+  check_fa(fa_decode_int8_kv_cache_gqa(q.data_ptr(), k_int8.data_ptr(), v_int8.data_ptr(), k_scale.data_ptr(),
+                                       v_scale.data_ptr(), out.data_ptr(), b, hq, hkv, n, d, cache_len,
+                                       ws_ptr(ws), ws_bytes(ws), cur_stream()));
+  return out;
+}
+
 // forward_decode_sliding_window_gqa (flash_attn_kernel.cu:4484-4535): keys k < sink_size
 // plus the window [max(0, min(cache_len+1, N) - window_size), cache_len]; `causal` is unused.
 at::Tensor forward_decode_sliding_window_gqa(at::Tensor q, at::Tensor k, at::Tensor v, bool causal, int cache_len,
@@ -651,6 +689,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_varlen_prefill_fp16", &forward_varlen_prefill_fp16, "Packed varlen prefill (MI355X MFMA)");
   m.def("forward_varlen_prefill_fp16_stream", &forward_varlen_prefill_fp16_stream,
         "Packed varlen prefill on a given stream");
+  m.def("forward_decode_int8_kv_cache_gqa", &forward_decode_int8_kv_cache_gqa,
+        "GQA decode with an INT8 KV cache and per-token scales (MI355X split-KV)");
   m.def("forward_decode_sliding_window_gqa", &forward_decode_sliding_window_gqa,
         "Sliding-window + attention-sink GQA decode (MI355X split-KV)");
   m.def("async_h2d_transfer", &async_h2d_transfer, "Async host-to-device copy from pinned memory");
@@ -659,7 +699,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pipeline_decode_step_out", &pipeline_decode_step_out,
         "GQA decode into out on one stream, H2D copies on another");
   for (const char* name : {"forward", "forward_with_lse", "forward_fp16_with_lse", "backward",
-                           "speculative_verify", "forward_decode_int8_kv_cache_gqa", "token_eviction",
+                           "speculative_verify", "token_eviction",
                            "cross_gpu_allreduce_fp16", "scatter_heads",
                            "gather_heads"}) {
     std::string n(name);

@@ -30,7 +30,7 @@
 
 namespace fa {
 
-enum DecodeMode : int { kModeDecode = 0, kModeCB = 1, kModePaged = 2, kModeInt8 = 3 };
+enum DecodeMode : int { kModeDecode = 0, kModeCB = 1, kModePaged = 2, kModeInt8 = 3, kModeInt8KV = 4 };
 
 constexpr int kDecWaves = 4;
 constexpr int kDecThreads = kDecWaves * 64;
@@ -59,6 +59,10 @@ struct DecodeParams {
   const half_t* q;
   const half_t* k;
   const half_t* v;
+  const int8_t* k8;            // INT8 KV cache: codes [B, H_KV, N, D]
+  const int8_t* v8;
+  const half_t* k_sc;          // INT8 KV cache: per-token scales [B, H_KV, N]
+  const half_t* v_sc;
   half_t* o;
   const int32_t* lens;         // CB: cache_lens; paged: seq_lens
   const int32_t* block_table;  // paged
@@ -115,6 +119,38 @@ __device__ __forceinline__ void quant8(u32x4 raw, float inv, int& lo, int& hi) {
   for (int j = 0; j < 8; ++j) r[j] = quant_rh(__builtin_fmaf(static_cast<float>(h[j]), inv, 0.0f));
   lo = pack4_i8(r[0], r[1], r[2], r[3]);
   hi = pack4_i8(r[4], r[5], r[6], r[7]);
+}
+
+// Eight int8 codes starting at column `col` of a row of length `d` (zero past d);
+// VEC: one unconditional 8-byte load (col + 8 <= d, 8-byte aligned address).
+template <bool VEC>
+__device__ __forceinline__ u32x2 load_i8x8(const int8_t* row, int col, int d) {
+  if constexpr (VEC) {
+    (void)d;
+    return *reinterpret_cast<const u32x2*>(row + col);
+  } else {
+    uint32_t w[2] = {0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (col + j < d) w[j >> 2] |= static_cast<uint32_t>(static_cast<uint8_t>(row[col + j])) << (8 * (j & 3));
+    return u32x2{w[0], w[1]};
+  }
+}
+
+// Eight int8 codes c -> eight fp16 half(c * s), as the reference's
+// __float2half((float)c * scale).  c * s is exact in fp32 (8-bit by 11-bit
+// significands); here it is formed as fma(u, s, -128 s) with u = c + 128 (the
+// code's byte with its top bit flipped, converted by v_cvt_f32_ubyte), whose
+// single rounding of an exactly representable value is exact, then rounded to
+// fp16 to nearest even.
+__device__ __forceinline__ u32x4 dequant_i8x8(u32x2 raw, float s) {
+  const u32x2 x = raw ^ u32x2{0x80808080u, 0x80808080u};
+  const float nb = -128.0f * s;
+  half8_t h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    h[j] = static_cast<half_t>(fmaf(static_cast<float>((x[j >> 2] >> (8 * (j & 3))) & 0xFFu), s, nb));
+  return __builtin_bit_cast(u32x4, h);
 }
 
 // Per-wave LDS scratch used to hand probabilities from the MFMA layout (lane =
@@ -288,6 +324,32 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     u32x4 k[T16][NC];
     u32x4 v[UV];
   };
+  // INT8 KV cache: one iteration's raw codes (K in the MFMA layout, V in the row
+  // layout, eight codes per 8-byte load) and the scales of their token rows.
+  struct Tile8 {
+    u32x2 k[T16][NC];
+    u32x2 v[UV];
+    float ks[T16];
+    float vs[UV];
+  };
+  auto load_tile8 = [&](Tile8& T, int t0) {
+    const int8_t* kh = p.k8 + kv_head_base;
+    const int8_t* vh = p.v8 + kv_head_base;
+    const size_t sbase = (static_cast<size_t>(b) * p.H_KV + hkv) * static_cast<size_t>(p.N);
+#pragma unroll
+    for (int tt = 0; tt < T16; ++tt) {
+      const int t = min(t0 + 16 * tt + l16, klast);
+      T.ks[tt] = static_cast<float>(p.k_sc[sbase + t]);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) T.k[tt][c] = load_i8x8<VEC>(kh + static_cast<size_t>(t) * D, 32 * c + 8 * q4, D);
+    }
+#pragma unroll
+    for (int u = 0; u < UV; ++u) {
+      const int t = min(t0 + u * RPW + rg, klast);
+      T.vs[u] = static_cast<float>(p.v_sc[sbase + t]);
+      T.v[u] = load_i8x8<VEC>(vh + static_cast<size_t>(t) * D, col, D);
+    }
+  };
   // -- loads: rows past k1 are clamped to k1-1 (always valid memory) and their
   //    scores are masked in compute_tile.
   auto load_tile = [&](Tile& T, int t0) {
@@ -440,7 +502,18 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   const int stride = kDecWaves * TK;
   for (int t0 = k0 + wave * TK; t0 < k1; t0 += stride) {
     Tile A;
-    load_tile(A, t0);
+    if constexpr (MODE == kModeInt8KV) {
+      Tile8 R;
+      load_tile8(R, t0);
+#pragma unroll
+      for (int tt = 0; tt < T16; ++tt)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) A.k[tt][c] = dequant_i8x8(R.k[tt][c], R.ks[tt]);
+#pragma unroll
+      for (int u = 0; u < UV; ++u) A.v[u] = dequant_i8x8(R.v[u], R.vs[u]);
+    } else {
+      load_tile(A, t0);
+    }
     compute_tile(A, t0);
   }
 
@@ -734,7 +807,8 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
     p.ws_o = reinterpret_cast<float*>(base + wl.o);
   }
   // Vector path: D fills the padded width exactly and every row starts 16-byte aligned.
-  const bool vec = (p.D == pl.dp) && aligned16(p.q) && aligned16(p.k) && aligned16(p.v);
+  const bool vec = (p.D == pl.dp) && aligned16(p.q) &&
+                   (MODE == kModeInt8KV ? aligned8(p.k8) && aligned8(p.v8) : aligned16(p.k) && aligned16(p.v));
   const long long units = static_cast<long long>(p.B) * p.H_KV * pl.num_hg;
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (long long u0 = 0; u0 < units; u0 += static_cast<long long>(kCounterSlots)) {
@@ -882,4 +956,27 @@ extern "C" int fa_decode_int8_gqa(const void* q, const void* k, const void* v, v
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
   p.fixed_len = cache_len + 1;
   return run_decode<kModeInt8>(fn, p, N, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fa_decode_int8_kv_cache_gqa(const void* q, const void* k_int8, const void* v_int8,
+                                          const void* k_scale, const void* v_scale, void* o, int B, int H_Q,
+                                          int H_KV, int N, int D, int cache_len, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  const char* fn = "fa_decode_int8_kv_cache_gqa";
+  int rc = check_common(fn, B, H_Q, H_KV, D);
+  if (rc != FA_OK) return rc;
+  if (N <= 0) return set_error(FA_ERR_INVALID_ARG, "%s: N must be positive", fn);
+  if (B > 0 && (!q || !k_int8 || !v_int8 || !k_scale || !v_scale || !o))
+    return set_error(FA_ERR_INVALID_ARG, "%s: null pointer", fn);
+  DecodeParams p = {};
+  p.q = static_cast<const half_t*>(q);
+  p.k8 = static_cast<const int8_t*>(k_int8);
+  p.v8 = static_cast<const int8_t*>(v_int8);
+  p.k_sc = static_cast<const half_t*>(k_scale);
+  p.v_sc = static_cast<const half_t*>(v_scale);
+  p.o = static_cast<half_t*>(o);
+  p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
+  // keys k <= cache_len always (cache_len unchecked: past N every key, below 0 none -> NaN)
+  p.fixed_len = static_cast<int>(std::min<long long>(std::max<long long>(static_cast<long long>(cache_len) + 1, 0), N));
+  return run_decode<kModeInt8KV>(fn, p, N, workspace, workspace_bytes, stream);
 }

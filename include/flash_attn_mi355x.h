@@ -91,6 +91,20 @@ int fa_decode_fp16(const void* q, const void* k, const void* v, void* o,
                    void* stream);
 
 /*
+ * GQA decode against an INT8 KV cache with per-token fp16 scales.
+ *   k_int8/v_int8 int8 [B, H_KV, N, D]; k_scale/v_scale fp16 [B, H_KV, N].
+ *   Element (t, d) is used as half(code * scale[t]); keys k <= cache_len are
+ *   attended (cache_len unchecked: >= N attends all N keys, < 0 none -> NaN).
+ *   Workspace as for fa_decode_fp16 (max_len = N).
+ * Replaces flash_attn_kernel_decode_int8_kv_cache_gqa (flash_attn_kernel.cu:4020-4159)
+ * behind flash_attn_forward_decode_int8_kv_cache_gqa (:4161-4221, bound at flash_attn.cpp:249).
+ */
+int fa_decode_int8_kv_cache_gqa(const void* q, const void* k_int8, const void* v_int8,
+                                const void* k_scale, const void* v_scale, void* o, int B,
+                                int H_Q, int H_KV, int N, int D, int cache_len,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Sliding-window (+ attention-sink) GQA decode against a contiguous cache.
  *   Attends key k iff k < sink_size, or window_start <= k <= cache_len with
  *   window_start = max(0, min(cache_len + 1, N) - window_size); no keys -> NaN.

@@ -599,3 +599,43 @@ def test_decode_sliding_window_validation(fa):
     kv2 = torch.zeros(1, 2, 32, 64, dtype=torch.float16, device=DEV)
     with pytest.raises(RuntimeError):
         fa.forward_decode_sliding_window_gqa(q2, kv2, kv2, True, 10, 4, 0)  # q_len != 1
+
+
+# ---------------------------------------------------------------- INT8 KV-cache decode
+
+def _int8_cache(g, b, hkv, n, d):
+    """Per-token absmax/127 quantization of N(0,1) K/V (test_kv_compress.py:7-18 convention),
+    with the extreme code -128 planted in a few places."""
+    k, v = randn(g, b, hkv, n, d).float(), randn(g, b, hkv, n, d).float()
+    ks, vs = k.abs().amax(-1) / 127, v.abs().amax(-1) / 127
+    k8 = torch.clamp(torch.round(k / ks.unsqueeze(-1)), -127, 127).to(torch.int8)
+    v8 = torch.clamp(torch.round(v / vs.unsqueeze(-1)), -127, 127).to(torch.int8)
+    k8.view(-1)[::97] = -128
+    v8.view(-1)[::89] = -128
+    return k8, v8, ks.half(), vs.half()
+
+
+@pytest.mark.parametrize("b,hq,hkv,n,d,cache_len", [
+    (2, 8, 2, 512, 64, 300), (1, 32, 8, 4097, 128, 4096), (2, 4, 4, 300, 256, 299),
+    (1, 8, 2, 200, 80, 150),      # odd D: element-wise path
+    (1, 4, 1, 64, 128, 500),      # cache_len >= N: every key
+    (2, 4, 2, 64, 64, -1),        # no key -> NaN
+])
+def test_decode_int8_kv_cache(fa, b, hq, hkv, n, d, cache_len):
+    g = gen(n + d)
+    q = randn(g, b, hq, 1, d)
+    k8, v8, ks, vs = _int8_cache(g, b, hkv, n, d)
+    out = fa.forward_decode_int8_kv_cache_gqa(*cuda(q, k8, v8, ks, vs), cache_len)
+    assert_close(out, A.decode_int8_kv_cache(q, k8, v8, ks, vs, cache_len), what="int8 kv cache")
+
+
+def test_decode_int8_kv_cache_validation(fa):
+    q = torch.zeros(1, 4, 1, 64, dtype=torch.float16, device=DEV)
+    k8 = torch.zeros(1, 2, 32, 64, dtype=torch.int8, device=DEV)
+    s = torch.zeros(1, 2, 32, dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_int8_kv_cache_gqa(q, k8.half(), k8, s, s, 3)   # k not int8
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_int8_kv_cache_gqa(q, k8, k8, s.float(), s, 3)  # scale not fp16
+    with pytest.raises(RuntimeError):
+        fa.forward_decode_int8_kv_cache_gqa(q, k8, k8, s[:, :, :16].contiguous(), s, 3)  # scale length
