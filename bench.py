@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention hot path on the BASELINE configs.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b] [--no-cpu]
 
 Prints ONE JSON line.  The headline ``value`` is BASELINE configs[1]: GQA decode
 via forward_decode_gqa_fp16, Q [1,32,1,128], K/V [1,8,4097,128] fp16,
@@ -15,7 +15,9 @@ and tokens/s (decode) or TFLOP/s (prefill), the ``roofline`` object for the
 headline kernel (timed with HIP events on the stream the kernel runs on), and
 ``cpu_baseline``: the CPU oracle (PyTorch eager fp32 math attention with the
 reference's masking, oracle/attention.py) timed on this host on a bounded
-sample of the same workload.
+sample of the same workload.  Configs 6a/6b (INT8 KV-cache and sliding-window
+decode) measure the next-row entry points at bandwidth-relevant shapes; they
+are not BASELINE configs.
 """
 from __future__ import annotations
 
@@ -43,7 +45,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5a,5b")
+    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
@@ -240,6 +242,53 @@ def cfg5b_int8(fa, torch, steps, warmup, nsets=5):
                 rotating_sets=nsets), sets[0]
 
 
+def cfg6a_int8_kv_cache(fa, torch, steps, warmup, nsets=4):
+    """forward_decode_int8_kv_cache_gqa on config 5b's shape with an int8 cache (per-token
+    absmax/127 fp16 scales): half the K/V bytes of the fp16 cache."""
+    B, HQ, HKV, N, D, CL = 16, 32, 8, 2049, 128, 2048
+    gg = torch.Generator(device="cuda").manual_seed(61)
+    sets = []
+    for _ in range(nsets):
+        q = torch.randn(B, HQ, 1, D, generator=gg, device="cuda").half()
+        kv = []
+        for _ in range(2):
+            x = torch.randn(B, HKV, N, D, generator=gg, device="cuda")
+            sc = (x.abs().amax(-1, keepdim=True) / 127.0).clamp(min=1e-8)
+            kv += [(x / sc).round().clamp(-128, 127).to(torch.int8).contiguous(), sc.squeeze(-1).half().contiguous()]
+        sets.append((q, kv[0], kv[2], kv[1], kv[3]))
+
+    def step(i):
+        q, k8, v8, ks, vs = sets[i % nsets]
+        fa.forward_decode_int8_kv_cache_gqa(q, k8, v8, ks, vs, CL)
+
+    ms = time_gpu(step, steps, warmup)
+    total = 2.0 * B * HKV * (CL + 1) * (D + 2) + 2.0 * B * HQ * D * 2
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="forward_decode_int8_kv_cache_gqa B=16 Hq=32 Hkv=8 N=2049 D=128 cache_len=2048 int8 K/V + fp16 per-token scales",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total, tokens_per_s=B / (ms * 1e-3),
+                rotating_sets=nsets), sets[0]
+
+
+def cfg6b_sliding_window(fa, torch, steps, warmup, nsets=3):
+    """forward_decode_sliding_window_gqa: B=16, 32:8 heads, N=8193, D=128, cache_len=8192,
+    window 2048 + 64 sink tokens (only those keys are read)."""
+    B, HQ, HKV, N, D, CL, W, S = 16, 32, 8, 8193, 128, 8192, 2048, 64
+    gg = torch.Generator(device="cuda").manual_seed(62)
+    sets = [tuple(torch.randn(*shape, generator=gg, device="cuda").half()
+                  for shape in ((B, HQ, 1, D), (B, HKV, N, D), (B, HKV, N, D))) for _ in range(nsets)]
+
+    def step(i):
+        q, k, v = sets[i % nsets]
+        fa.forward_decode_sliding_window_gqa(q, k, v, True, CL, W, S)
+
+    ms = time_gpu(step, steps, warmup)
+    total = 2.0 * B * HKV * (W + S) * D * 2 + 2.0 * B * HQ * D * 2
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="forward_decode_sliding_window_gqa B=16 Hq=32 Hkv=8 N=8193 D=128 cache_len=8192 window=2048 sink=64",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total, tokens_per_s=B / (ms * 1e-3),
+                rotating_sets=nsets), (sets[0], CL, W, S)
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_cfg2(torch, sample, budget_s=12.0):
@@ -303,6 +352,23 @@ def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
         by = 2.0 * len(idx) * k.shape[1] * (cl + 1) * k.shape[3] * 2
         out["5b"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
                          sample="2 of 16 sequences")
+    if "6a" in samples:
+        q, k8, v8, ks, vs = samples["6a"]
+        idx = [0, 1]
+        args = [t[idx].cpu() for t in (q, k8, v8, ks, vs)]
+        cl = k8.shape[2] - 1
+        sec, _ = time_cpu(lambda: A.decode_int8_kv_cache(*args, cl), budget_s)
+        by = 2.0 * len(idx) * k8.shape[1] * (cl + 1) * (k8.shape[3] + 2)
+        out["6a"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
+                         sample="2 of 16 sequences")
+    if "6b" in samples:
+        (q, k, v), cl, w, sk = samples["6b"]
+        idx = [0, 1]
+        qs, ks, vs = q[idx].cpu(), k[idx].cpu(), v[idx].cpu()
+        sec, _ = time_cpu(lambda: A.decode_sliding_window(qs, ks, vs, cl, w, sk), budget_s)
+        by = 2.0 * len(idx) * k.shape[1] * (w + sk) * k.shape[3] * 2
+        out["6b"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
+                         sample="2 of 16 sequences (the whole cache is read on the CPU)")
     return out
 
 
@@ -342,8 +408,10 @@ def main():
         "4": lambda: cfg4_paged(fa, torch, 30, 5),
         "5a": lambda: cfg5a_varlen(fa, torch, 20, 3),
         "5b": lambda: cfg5b_int8(fa, torch, 100, 10),
+        "6a": lambda: cfg6a_int8_kv_cache(fa, torch, 100, 10),
+        "6b": lambda: cfg6b_sliding_window(fa, torch, 100, 10),
     }
-    for c in ["1", "2", "3", "4", "5a", "5b"]:
+    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b"]:
         if c not in want:
             continue
         log(f"config {c} ...")

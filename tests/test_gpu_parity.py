@@ -639,3 +639,30 @@ def test_decode_int8_kv_cache_validation(fa):
         fa.forward_decode_int8_kv_cache_gqa(q, k8, k8, s.float(), s, 3)  # scale not fp16
     with pytest.raises(RuntimeError):
         fa.forward_decode_int8_kv_cache_gqa(q, k8, k8, s[:, :, :16].contiguous(), s, 3)  # scale length
+
+
+@pytest.mark.parametrize("b,hq,hkv,n,d", [(1, 8, 8, 128, 64), (2, 8, 2, 256, 64), (4, 16, 4, 512, 128)])
+def test_int8_kv_cache_reference_case(fa, b, hq, hkv, n, d):
+    """test_kv_compress.py:21-60: its quantizer (per-token absmax/127, scale >= 1e-8, codes
+    clamped to [-128, 127]); the output matches the oracle on the int8 cache and stays within
+    the reference's 0.1 of the fp16 decode on the unquantized cache."""
+    g = gen(42)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+
+    def quant(x):
+        s = (x.float().abs().amax(-1, keepdim=True) / 127.0).clamp(min=1e-8)
+        return (x.float() / s).round().clamp(-128, 127).to(torch.int8), s.squeeze(-1).half()
+
+    k8, ks = quant(k)
+    v8, vs = quant(v)
+    out = fa.forward_decode_int8_kv_cache_gqa(*cuda(q, k8, v8, ks, vs), n - 1)
+    assert_close(out, A.decode_int8_kv_cache(q, k8, v8, ks, vs, n - 1), what="int8 kv reference case")
+    assert (out.float().cpu() - A.decode(q, k, v, True, n - 1)).abs().max().item() < 0.1
+
+
+def test_sliding_window_reference_case(fa):
+    """test_kv_compress.py:231-290: B=2, 8:2 heads, N=256, D=64, cache_len=N-1, window 64, sink 4."""
+    g = gen(42)
+    q, k, v = randn(g, 2, 8, 1, 64), randn(g, 2, 2, 256, 64), randn(g, 2, 2, 256, 64)
+    out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, 255, 64, 4)
+    assert_close(out, A.decode_sliding_window(q, k, v, 255, 64, 4), what="sliding reference case")
