@@ -27,18 +27,21 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["decode.hip", "prefill.hip"]
+KERNEL_SOURCES = ["decode.hip", "prefill.hip", "train.hip"]
 HOST_SOURCES = ["capi.cpp"]
 
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # Keep the compiler from forming packed-fp32 VALU ops (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in ordinary VGPRs: without it the compiler parks them in
-    # AGPRs and copies them back and forth around every branch of the kernels.
-    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall", "-Wno-unused-variable", "-Wno-unused-but-set-variable",
 ]
+# MFMA accumulators in ordinary VGPRs: without it the compiler parks them in
+# AGPRs and copies them back and forth around every branch of the kernels.
+# The training kernels (train.hip) only accumulate and store their MFMA results,
+# so they keep the accumulators in AGPRs and the VGPRs for operands.
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+SOURCE_FLAGS = {"decode.hip": VGPR_FORM, "prefill.hip": VGPR_FORM}
 
 
 def _run(cmd):
@@ -68,7 +71,7 @@ def build_library(verbose: bool = True) -> str:
     jobs = []
     for src in KERNEL_SOURCES + HOST_SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-        cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(REPO_DIR, "include")]
+        cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-I", os.path.join(REPO_DIR, "include")]
         if src.endswith(".cpp"):
             cmd += ["-x", "hip"]
         cmd += ["-c", os.path.join(CSRC, src), "-o", obj]

@@ -507,6 +507,94 @@ at::Tensor forward_varlen_prefill_fp16_stream(at::Tensor q, at::Tensor k, at::Te
 }
 
 // ---------------------------------------------------------------------------
+// Training: log-sum-exp forwards and the backward.
+
+void check_lse_forward(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, at::ScalarType dt,
+                       const char* dtype_msg) {
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  check_mha_input_shapes(q, k, v);
+  TORCH_CHECK(q.dtype() == dt, dtype_msg);
+  TORCH_CHECK(q.size(3) <= kMaxD, "D must be less than or equal to MAX_D(128)");
+}
+
+std::tuple<at::Tensor, at::Tensor> forward_fp32_impl(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
+                                                     bool want_lse) {
+  check_lse_forward(q, k, v, at::kFloat, "q, k, v must be float32");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  at::Tensor lse;
+  if (want_lse) lse = at::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat));
+  check_fa(fa_prefill_fp32(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                           want_lse ? lse.data_ptr<float>() : nullptr, to_int(q.size(0), "B"),
+                           to_int(q.size(1), "H"), to_int(q.size(2), "N"), to_int(q.size(3), "D"),
+                           causal ? 1 : 0, cur_stream()));
+  return std::make_tuple(out, lse);
+}
+
+// forward (flash_attn_kernel.cu:508-550): fp32 MHA forward.
+at::Tensor forward_fp32(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  return std::get<0>(forward_fp32_impl(q, k, v, causal, false));
+}
+
+// forward_with_lse (flash_attn_kernel.cu:1964-2006): fp32 forward + LSE [B, H, N].
+std::tuple<at::Tensor, at::Tensor> forward_with_lse(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  return forward_fp32_impl(q, k, v, causal, true);
+}
+
+// forward_fp16_with_lse (flash_attn_kernel.cu:2008-2050): fp16 forward + fp32 LSE [B, H, N].
+std::tuple<at::Tensor, at::Tensor> forward_fp16_with_lse(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  check_lse_forward(q, k, v, at::kHalf, "q, k, v must be float16");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto out = at::empty_like(q);
+  auto lse = at::empty({q.size(0), q.size(1), q.size(2)}, q.options().dtype(at::kFloat));
+  check_fa(fa_prefill_fp16_lse(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr<float>(),
+                               to_int(q.size(0), "B"), to_int(q.size(1), "H"), to_int(q.size(2), "N"),
+                               to_int(q.size(3), "D"), causal ? 1 : 0, cur_stream()));
+  return std::make_tuple(out, lse);
+}
+
+// backward (flash_attn_kernel.cu:2173-2264): dq, dk, dv in q's dtype.
+std::tuple<at::Tensor, at::Tensor, at::Tensor> backward(at::Tensor dout, at::Tensor q, at::Tensor k, at::Tensor v,
+                                                        at::Tensor out, at::Tensor logsumexp, bool causal) {
+  CHECK_INPUT(dout);
+  CHECK_INPUT(q);
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  CHECK_INPUT(out);
+  CHECK_INPUT(logsumexp);
+  check_mha_input_shapes(q, k, v);
+  TORCH_CHECK(dout.sizes() == q.sizes(), "dout and q must have the same shape");
+  TORCH_CHECK(out.sizes() == q.sizes(), "out and q must have the same shape");
+  CHECK_SAME_DEVICE(dout, q);
+  CHECK_SAME_DEVICE(out, q);
+  CHECK_SAME_DEVICE(logsumexp, q);
+  CHECK_SAME_DTYPE(dout, q);
+  CHECK_SAME_DTYPE(out, q);
+  TORCH_CHECK(q.dtype() == at::kFloat || q.dtype() == at::kHalf, "q, k, v must be float32 or float16");
+  TORCH_CHECK(logsumexp.dtype() == at::kFloat, "logsumexp must be float32");
+  const auto B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  TORCH_CHECK(D <= kMaxD, "D must be less than or equal to MAX_D(128)");
+  CHECK_DIM(logsumexp, 3);
+  TORCH_CHECK(logsumexp.size(0) == B && logsumexp.size(1) == H && logsumexp.size(2) == N,
+              "logsumexp shape must be [B, H, N]");
+  HIPGuardMasqueradingAsCUDA guard(q.device());
+  auto dq = at::empty_like(q);
+  auto dk = at::empty_like(k);
+  auto dv = at::empty_like(v);
+  const int b = to_int(B, "B"), h = to_int(H, "H"), n = to_int(N, "N"), d = to_int(D, "D");
+  const size_t ws_bytes = fa_backward_workspace_size(b, h, n);
+  at::Tensor ws;
+  if (ws_bytes > 0) ws = at::empty({static_cast<int64_t>(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
+  auto fn = q.dtype() == at::kHalf ? fa_backward_fp16 : fa_backward_fp32;
+  check_fa(fn(dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+              logsumexp.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), b, h, n, d,
+              causal ? 1 : 0, ws_ptr(ws), ws_bytes, cur_stream()));
+  return std::make_tuple(dq, dk, dv);
+}
+
+// ---------------------------------------------------------------------------
 // Names of the reference module that are outside the MI355X hot path.
 
 void not_implemented(const char* name) {
@@ -698,8 +786,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("pipeline_decode_step", &pipeline_decode_step, "GQA decode on one stream, H2D copies on another");
   m.def("pipeline_decode_step_out", &pipeline_decode_step_out,
         "GQA decode into out on one stream, H2D copies on another");
-  for (const char* name : {"forward", "forward_with_lse", "forward_fp16_with_lse", "backward",
-                           "speculative_verify", "token_eviction",
+  m.def("forward", &forward_fp32, "Flash attention forward, fp32 (MI355X fp32 MFMA)");
+  m.def("forward_with_lse", &forward_with_lse, "fp32 forward with logsumexp (MI355X)");
+  m.def("forward_fp16_with_lse", &forward_fp16_with_lse, "fp16 forward with logsumexp (MI355X MFMA)");
+  m.def("backward", &backward, "Attention backward for MHA, fp32/fp16 (MI355X MFMA)");
+  for (const char* name : {"speculative_verify", "token_eviction",
                            "cross_gpu_allreduce_fp16", "scatter_heads",
                            "gather_heads"}) {
     std::string n(name);

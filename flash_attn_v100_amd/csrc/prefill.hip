@@ -60,6 +60,7 @@ struct PrefillParams {
   const half_t* k;
   const half_t* v;
   half_t* o;
+  float* lse;                 // dense only: natural-log log-sum-exp [B, H_Q, N], written if non-null
   const int32_t* cu_seqlens;  // varlen only
   int B, H_Q, H_KV, N, D, G;
   int total, row_limit;       // varlen only
@@ -476,6 +477,12 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
     const int qrow = wq0 + 32 * rb + l32;
     if (qrow >= rows) continue;
     const float inv = 1.0f / lt;
+    if constexpr (!VARLEN) {
+      // l is the sum of exp2(s c - m) against the running m, so m + log2(l) is
+      // the log2-sum-exp of the row whichever m the lazy rescaling settled on.
+      if (p.lse != nullptr && hi == 0)
+        p.lse[(static_cast<size_t>(b) * p.H_Q + h) * p.N + qrow] = (m_run[rb] + log2f(lt)) * 0.69314718055994531f;
+    }
     half_t* op = p.o + q_base + static_cast<size_t>(qrow) * stride;
 #pragma unroll
     for (int db = 0; db < DB; ++db) {
@@ -536,9 +543,8 @@ static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, Prefi
 
 using namespace fa;
 
-extern "C" int fa_prefill_fp16(const void* q, const void* k, const void* v, void* o, int B, int H_Q,
-                               int H_KV, int N, int D, int causal, void* stream) {
-  const char* fn = "fa_prefill_fp16";
+static int prefill_dense(const char* fn, const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                         int H_Q, int H_KV, int N, int D, int causal, void* stream) {
   if (B < 0 || N < 0 || H_Q <= 0 || H_KV <= 0 || D <= 0)
     return set_error(FA_ERR_INVALID_ARG, "%s: bad sizes (B=%d H_Q=%d H_KV=%d N=%d D=%d)", fn, B, H_Q, H_KV, N, D);
   if (H_Q < H_KV || H_Q % H_KV != 0)
@@ -551,12 +557,25 @@ extern "C" int fa_prefill_fp16(const void* q, const void* k, const void* v, void
   p.k = static_cast<const half_t*>(k);
   p.v = static_cast<const half_t*>(v);
   p.o = static_cast<half_t*>(o);
+  p.lse = lse;
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D; p.G = H_Q / H_KV;
   p.causal = causal ? 1 : 0;
   p.scale_log2 = (1.0f / sqrtf(static_cast<float>(D))) * kLog2e;
   // Vector path: D fills the padded width exactly and every row starts 16-byte aligned.
   const bool vec = (D == 64 || D == 128 || D == 256) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   return dispatch_prefill<false>(fn, D, vec, N, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fa_prefill_fp16(const void* q, const void* k, const void* v, void* o, int B, int H_Q,
+                               int H_KV, int N, int D, int causal, void* stream) {
+  return prefill_dense("fa_prefill_fp16", q, k, v, o, nullptr, B, H_Q, H_KV, N, D, causal, stream);
+}
+
+extern "C" int fa_prefill_fp16_lse(const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                                   int H, int N, int D, int causal, void* stream) {
+  if (lse == nullptr && B > 0 && N > 0)
+    return set_error(FA_ERR_INVALID_ARG, "fa_prefill_fp16_lse: null lse pointer");
+  return prefill_dense("fa_prefill_fp16_lse", q, k, v, o, lse, B, H, H, N, D, causal, stream);
 }
 
 extern "C" int fa_varlen_prefill_fp16(const void* q, const void* k, const void* v, void* o,

@@ -55,6 +55,56 @@ int fa_prefill_fp16(const void* q, const void* k, const void* v, void* o,
                     void* stream);
 
 /*
+ * fp16 MHA prefill that also returns the natural-log log-sum-exp of each
+ * query row's scaled scores, lse [B, H, N] fp32 (the statistic the backward
+ * consumes).  q/k/v/o [B, H, N, D], 1 <= D <= 256 (the binding keeps the
+ * reference's D <= 128).
+ * Replaces the launch behind forward_fp16_with_lse (flash_attn_kernel.cu:2008-2050,
+ * kernel flash_attn_kernel_fp16 with a non-null LSE, :1295-1297).
+ */
+int fa_prefill_fp16_lse(const void* q, const void* k, const void* v, void* o,
+                        float* lse, int B, int H, int N, int D, int causal,
+                        void* stream);
+
+/*
+ * fp32 MHA prefill (fp32 MFMA), optionally with log-sum-exp.
+ *   q/k/v/o fp32 [B, H, N, D], 1 <= D <= 128, B*H <= 65535; lse fp32 [B, H, N]
+ *   or NULL.  Causal masks key j > query i.
+ * Replaces the launches behind forward (flash_attn_kernel.cu:508-550) and
+ * forward_with_lse (:1964-2006), kernel flash_attn_kernel (:369-506).
+ */
+int fa_prefill_fp32(const void* q, const void* k, const void* v, void* o,
+                    float* lse, int B, int H, int N, int D, int causal,
+                    void* stream);
+
+/*
+ * Workspace bytes fa_backward_fp16/_fp32 need (one fp32 per query row).
+ */
+size_t fa_backward_workspace_size(int B, int H, int N);
+
+/*
+ * Attention backward for MHA: given dout, q, k, v, the forward output `out`
+ * and its log-sum-exp `lse` [B, H, N] fp32, writes dq, dk, dv (same shape and
+ * type as q).  fp16 variant: every tensor but lse is fp16 (gradients
+ * accumulate in fp32 and are rounded once); fp32 variant: all fp32.
+ * 1 <= D <= 128, B*H <= 65535.  Two launches on `stream` (dQ with the row
+ * statistic delta = rowsum(dout * out) into the workspace, then dK/dV);
+ * deterministic (no atomics).  The workspace needs no initialisation.
+ * Replaces flash_attn_backward (flash_attn_kernel.cu:2173-2264), kernels
+ * flash_attn_backward_tiled_kernel_fp32/_fp16 (:2056-2171).
+ */
+int fa_backward_fp16(const void* dout, const void* q, const void* k,
+                     const void* v, const void* out, const float* lse,
+                     void* dq, void* dk, void* dv, int B, int H, int N, int D,
+                     int causal, void* workspace, size_t workspace_bytes,
+                     void* stream);
+int fa_backward_fp32(const void* dout, const void* q, const void* k,
+                     const void* v, const void* out, const float* lse,
+                     void* dq, void* dk, void* dv, int B, int H, int N, int D,
+                     int causal, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
  * Packed variable-length prefill.
  *   q/k/v/o [total, H, D]; cu_seqlens int32 [batch + 1] in device memory.
  *   Sequence b owns rows [cu[b], cu[b+1]); only its first `row_limit` rows get

@@ -343,3 +343,54 @@ def decode_int8_kv_cache(q, k_i8, v_i8, k_scale, v_scale, cache_len: int,
     vd = dequant_int8_cache(v_i8, v_scale)
     mask = (torch.arange(n) > cache_len).view(1, 1, 1, n)
     return _attend(q, expand_kv(kd, q.shape[1]), expand_kv(vd, q.shape[1]), mask, compute_dtype)
+
+
+def _causal_mask(n: int) -> torch.Tensor:
+    """Square top-left causal mask, True where key > query (flash_attn_kernel.cu:445, :2084)."""
+    return torch.triu(torch.ones(n, n, dtype=torch.bool), diagonal=1)
+
+
+def prefill_lse(q, k, v, causal: bool, compute_dtype=torch.float32):
+    """``forward_with_lse`` (fp32) / ``forward_fp16_with_lse`` (fp16): MHA forward
+    plus ``LSE[b,h,i] = m_i + log(l_i)`` (flash_attn_kernel.cu:502-504, :1295-1297),
+    i.e. the natural-log log-sum-exp of the row's scaled, masked scores.
+
+    Returns ``(out, lse)``; out as :func:`prefill`, lse [B,H,N] in compute_dtype.
+    """
+    d = q.shape[-1]
+    n = q.shape[2]
+    scores = torch.matmul(q.to(compute_dtype), k.to(compute_dtype).transpose(-1, -2)) * (1.0 / math.sqrt(d))
+    if causal:
+        scores = scores.masked_fill(_causal_mask(n), float("-inf"))
+    lse = torch.logsumexp(scores, dim=-1)
+    out = torch.matmul(torch.exp(scores - lse.unsqueeze(-1)), v.to(compute_dtype))
+    return out, lse
+
+
+def backward(dout, q, k, v, out, lse, causal: bool, compute_dtype=torch.float64):
+    """``backward`` (flash_attn_kernel.cu:2173-2264; per-(query, key) kernels :2056-2171).
+
+    Uses the caller's ``out`` and ``lse`` as the reference does (it never
+    recomputes them).  For every unmasked pair (i, j) (causal masks j > i,
+    :2084):
+        p_ij   = exp(scale * q_i . k_j - LSE_i)                 (:2103)
+        delta_i = dO_i . O_i,   ds_ij = p_ij (dO_i . v_j - delta_i) scale   (:2104)
+        dQ_i += ds_ij k_j,  dK_j += ds_ij q_i,  dV_j += p_ij dO_i    (:2106-2110)
+    Returns ``(dq, dk, dv)`` in compute_dtype.
+    """
+    cd = compute_dtype
+    d = q.shape[-1]
+    n = q.shape[2]
+    scale = 1.0 / math.sqrt(d)
+    qf, kf, vf, dof, of = (t.to(cd) for t in (q, k, v, dout, out))
+    s = torch.matmul(qf, kf.transpose(-1, -2)) * scale
+    p = torch.exp(s - lse.to(cd).unsqueeze(-1))
+    if causal:
+        p = p.masked_fill(_causal_mask(n), 0.0)
+    delta = (dof * of).sum(-1, keepdim=True)
+    dp = torch.matmul(dof, vf.transpose(-1, -2))
+    ds = p * (dp - delta) * scale
+    dq = torch.matmul(ds, kf)
+    dk = torch.matmul(ds.transpose(-1, -2), qf)
+    dv = torch.matmul(p.transpose(-1, -2), dof)
+    return dq, dk, dv

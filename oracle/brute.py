@@ -267,3 +267,72 @@ def decode_int8_kv_cache(q, k_i8, v_i8, k_scale, v_scale, cache_len):
             g = h // (hq // hkv)
             out[b][h] = [_online_attend(q[b][h][0], kd[g], vd[g], lambda j: j > cache_len, scale, 64)]
     return out
+
+
+def prefill_lse(q, k, v, causal):
+    """forward_with_lse / forward_fp16_with_lse: the fp32 kernel's loop
+    (flash_attn_kernel.cu:421-504, tiles of TILE_K=32) keeping ``m_i`` and
+    ``l_i``; LSE = m_i + log(l_i) (:502-504).  Returns (out, lse) as nested lists
+    [B][H][N][D] and [B][H][N]."""
+    q, k, v = _tolist(q), _tolist(k), _tolist(v)
+    B, H, N, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    scale = 1.0 / math.sqrt(D)
+    out, lse = [], []
+    for b in range(B):
+        ob, lb = [], []
+        for h in range(H):
+            oh, lh = [], []
+            for i in range(N):
+                m_i, l_i = -FLT_MAX, 0.0
+                acc = [0.0] * D
+                for start in range(0, N, 32):
+                    js = [j for j in range(start, min(start + 32, N)) if not (causal and j > i)]
+                    if not js:
+                        continue
+                    sc = {j: sum(q[b][h][i][t] * k[b][h][j][t] for t in range(D)) * scale for j in js}
+                    m_new = max(m_i, max(sc.values()))
+                    alpha = 0.0 if m_i == -FLT_MAX else math.exp(m_i - m_new)
+                    acc = [alpha * a for a in acc]
+                    l_i *= alpha
+                    for j in js:
+                        p = math.exp(sc[j] - m_new)
+                        l_i += p
+                        for t in range(D):
+                            acc[t] += p * v[b][h][j][t]
+                    m_i = m_new
+                oh.append([a / l_i for a in acc])
+                lh.append(m_i + math.log(l_i))
+            ob.append(oh)
+            lb.append(lh)
+        out.append(ob)
+        lse.append(lb)
+    return out, lse
+
+
+def backward(dout, q, k, v, out, lse, causal):
+    """backward: the reference's one-thread-per-(query, key) kernel
+    (flash_attn_kernel.cu:2056-2111) as a loop over (b, h, i, j) with the
+    atomicAdd accumulations as +=.  Returns (dq, dk, dv) nested lists."""
+    dout, q, k, v, out, lse = (_tolist(x) for x in (dout, q, k, v, out, lse))
+    B, H, N, D = len(q), len(q[0]), len(q[0][0]), len(q[0][0][0])
+    scale = 1.0 / math.sqrt(D)
+    zeros = lambda: [[[[0.0] * D for _ in range(N)] for _ in range(H)] for _ in range(B)]
+    dq, dk, dv = zeros(), zeros(), zeros()
+    for b in range(B):
+        for h in range(H):
+            for i in range(N):
+                for j in range(N):
+                    if causal and j > i:
+                        continue
+                    qi, kj, vj = q[b][h][i], k[b][h][j], v[b][h][j]
+                    doi, oi = dout[b][h][i], out[b][h][i]
+                    score = sum(qi[t] * kj[t] for t in range(D))
+                    do_dot_v = sum(doi[t] * vj[t] for t in range(D))
+                    delta = sum(doi[t] * oi[t] for t in range(D))
+                    p = math.exp(score * scale - lse[b][h][i])
+                    ds = p * (do_dot_v - delta) * scale
+                    for t in range(D):
+                        dq[b][h][i][t] += ds * kj[t]
+                        dk[b][h][j][t] += ds * qi[t]
+                        dv[b][h][j][t] += p * doi[t]
+    return dq, dk, dv

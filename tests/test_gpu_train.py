@@ -1,0 +1,131 @@
+"""GPU parity of the training path: forward with log-sum-exp (fp32 and fp16),
+fp32 forward, and the backward (dq, dk, dv), against the CPU oracle.
+
+Cases follow the reference's test_backward.py (B=2, H=3, N=17, D=32; seeds 11
+for the LSE forwards, 7 for the backward, through the autograd wrapper) plus
+ragged lengths, D not a multiple of 8, D in {16..128} and longer sequences.
+Tolerances: fp32 max-abs 2e-4 + rtol 2e-4 (the reference's fp32 bound);
+fp16 forward max-abs 2e-3 + rtol 1e-2; fp16 LSE max-abs 2e-3; fp16 gradients
+max-abs 3e-2 + rtol 3e-2 (the reference's fp16 bound) and rel-L2 <= 1e-2.
+"""
+import pytest
+import torch
+
+from oracle import attention as A
+from tests.helpers import assert_close, randn, rel_l2
+
+pytestmark = pytest.mark.gpu
+F64 = torch.float64
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def cuda(*ts):
+    return [t.cuda().contiguous() for t in ts]
+
+
+SHAPES = [(2, 3, 17, 32), (1, 2, 1, 64), (1, 2, 33, 64), (1, 2, 129, 128), (2, 2, 200, 80),
+          (1, 1, 70, 36), (1, 2, 45, 16), (1, 3, 300, 128), (1, 2, 96, 100)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,n,d", SHAPES)
+def test_forward_with_lse_fp32(fa, causal, b, h, n, d):
+    g = gen(11 + n + d)
+    q, k, v = (randn(g, b, h, n, d, dtype=torch.float32) for _ in range(3))
+    out, lse = fa.forward_with_lse(*cuda(q, k, v), causal)
+    ro, rl = A.prefill_lse(q, k, v, causal, compute_dtype=F64)
+    assert out.dtype == torch.float32 and lse.dtype == torch.float32 and lse.shape == (b, h, n)
+    assert_close(out, ro, atol=2e-4, rtol=2e-4, what="forward_with_lse out")
+    assert_close(lse, rl, atol=2e-4, rtol=2e-4, what="forward_with_lse lse")
+    out2 = fa.forward(*cuda(q, k, v), causal)
+    assert torch.equal(out2, out)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,n,d", SHAPES)
+def test_forward_fp16_with_lse(fa, causal, b, h, n, d):
+    g = gen(11 + n + d)
+    q, k, v = (randn(g, b, h, n, d) for _ in range(3))
+    qc, kc, vc = cuda(q, k, v)
+    out, lse = fa.forward_fp16_with_lse(qc, kc, vc, causal)
+    ro, rl = A.prefill_lse(q, k, v, causal, compute_dtype=F64)
+    assert out.dtype == torch.float16 and lse.dtype == torch.float32 and lse.shape == (b, h, n)
+    assert_close(out, ro, what="forward_fp16_with_lse out")
+    assert_close(lse, rl, atol=2e-3, rtol=0, what="forward_fp16_with_lse lse")
+    # same kernel as forward_fp16: identical output
+    assert torch.equal(out, fa.forward_fp16(qc, kc, vc, causal))
+
+
+def _check_grads(got, ref, fp16, what):
+    for name, a, r in zip(("dq", "dk", "dv"), got, ref):
+        if fp16:
+            assert_close(a, r, atol=3e-2, rtol=3e-2, what=f"{what} {name}")
+            if r.double().norm() > 1e-3:  # rel-L2 is undefined for an all-zero gradient (N=1 dq)
+                assert rel_l2(a, r) <= 1e-2, (what, name, rel_l2(a, r))
+        else:
+            assert_close(a, r, atol=2e-4, rtol=2e-4, what=f"{what} {name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("causal", [True, False])
+def test_backward_reference_case(fa, dtype, causal):
+    """test_backward.py:33-71 through the autograd wrapper (flash_attn_autograd.flash_attn)."""
+    from flash_attn_autograd import flash_attn
+
+    g = gen(7)
+    B, H, N, D = 2, 3, 17, 32
+    q, k, v, do = (randn(g, B, H, N, D, dtype=dtype) for _ in range(4))
+    qg, kg, vg = (t.cuda().requires_grad_(True) for t in (q, k, v))
+    out = flash_attn(qg, kg, vg, causal=causal)
+    out.backward(do.cuda())
+    ro, rl = A.prefill_lse(q, k, v, causal, compute_dtype=F64)
+    ref = A.backward(do, q, k, v, ro, rl, causal)
+    assert qg.grad.dtype == dtype
+    _check_grads((qg.grad, kg.grad, vg.grad), ref, dtype == torch.float16, "autograd")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("b,h,n,d", SHAPES[1:] + [(1, 2, 512, 128), (2, 2, 257, 64)])
+def test_backward_shapes(fa, dtype, causal, b, h, n, d):
+    g = gen(300 + n * 3 + d)
+    q, k, v, do = (randn(g, b, h, n, d, dtype=dtype) for _ in range(4))
+    qc, kc, vc, dc = cuda(q, k, v, do)
+    fwd = fa.forward_fp16_with_lse if dtype == torch.float16 else fa.forward_with_lse
+    out, lse = fwd(qc, kc, vc, causal)
+    dq, dk, dv = fa.backward(dc, qc, kc, vc, out, lse, causal)
+    # the oracle takes the same out/lse the kernels were given
+    ref = A.backward(do, q, k, v, out.cpu(), lse.cpu(), causal)
+    _check_grads((dq, dk, dv), ref, dtype == torch.float16, f"backward {b,h,n,d}")
+
+
+def test_backward_deterministic(fa):
+    g = gen(5)
+    q, k, v, do = (randn(g, 1, 4, 333, 64) for _ in range(4))
+    qc, kc, vc, dc = cuda(q, k, v, do)
+    out, lse = fa.forward_fp16_with_lse(qc, kc, vc, True)
+    a = fa.backward(dc, qc, kc, vc, out, lse, True)
+    b = fa.backward(dc, qc, kc, vc, out, lse, True)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_training_validation_errors(fa):
+    q = torch.randn(1, 2, 8, 256, device="cuda", dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        fa.forward_fp16_with_lse(q, q, q, True)  # D > 128
+    q32 = torch.randn(1, 2, 8, 64, device="cuda")
+    with pytest.raises(RuntimeError):
+        fa.forward_with_lse(q32.half(), q32.half(), q32.half(), True)  # dtype
+    with pytest.raises(RuntimeError):
+        fa.forward(q32, q32[:, :1].contiguous(), q32, True)  # shapes
+    out, lse = fa.forward_with_lse(q32, q32, q32, True)
+    with pytest.raises(RuntimeError):
+        fa.backward(q32, q32, q32, q32, out, lse[:, :1].contiguous(), True)  # lse shape
+    with pytest.raises(RuntimeError):
+        fa.backward(q32, q32, q32, q32, out, lse.double(), True)  # lse dtype
+    with pytest.raises(RuntimeError):
+        fa.backward(q32.half(), q32, q32, q32, out, lse, True)  # dout dtype

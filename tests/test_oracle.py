@@ -331,3 +331,89 @@ def test_int8_kv_cache_exact_scales_reduce_to_decode():
     vs = torch.full((1, 2, 33), 2.0 ** -5).half()
     kd, vd = k_i8.double() * 2.0 ** -6, v_i8.double() * 2.0 ** -5
     close(A.decode_int8_kv_cache(q, k_i8, v_i8, ks, vs, 20, F64), A.decode(q, kd, vd, True, 20, F64))
+
+
+# ---------------------------------------------------------------- training path (LSE forward, backward)
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("n,d", [(5, 4), (33, 8), (40, 3)])
+def test_prefill_lse_vs_brute(causal, n, d):
+    g = torch.Generator().manual_seed(100 + n + d)
+    q, k, v = (randn(g, 1, 2, n, d, dtype=F64) for _ in range(3))
+    out, lse = A.prefill_lse(q, k, v, causal, compute_dtype=F64)
+    bo, bl = Bt.prefill_lse(q, k, v, causal)
+    close(out, bo)
+    close(lse, bl)
+    # out equals the plain prefill restatement
+    close(out, A.prefill(q, k, v, causal, compute_dtype=F64))
+
+
+def test_prefill_lse_closed_forms():
+    g = torch.Generator().manual_seed(7)
+    d = 8
+    q = randn(g, 1, 1, 6, d, dtype=F64)
+    k1 = randn(g, 1, 1, 1, d, dtype=F64)
+    kk = k1.expand(1, 1, 6, d).contiguous()
+    v = randn(g, 1, 1, 6, d, dtype=F64)
+    _, lse = A.prefill_lse(q, kk, v, causal=False, compute_dtype=F64)
+    # identical keys: LSE_i = s_i + log(N)
+    s = (q * k1).sum(-1) / d ** 0.5
+    close(lse, s + torch.log(torch.tensor(6.0, dtype=F64)))
+    # causal row 0 sees only key 0: LSE_0 = s_00
+    _, lse_c = A.prefill_lse(q, v, v, causal=True, compute_dtype=F64)
+    close(lse_c[..., 0], (q[..., 0, :] * v[..., 0, :]).sum(-1) / d ** 0.5)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("n,d", [(5, 4), (17, 8), (9, 3)])
+def test_backward_vs_brute(causal, n, d):
+    g = torch.Generator().manual_seed(200 + n * d)
+    q, k, v, do = (randn(g, 1, 2, n, d, dtype=F64) for _ in range(4))
+    out, lse = A.prefill_lse(q, k, v, causal, compute_dtype=F64)
+    got = A.backward(do, q, k, v, out, lse, causal)
+    ref = Bt.backward(do, q, k, v, out, lse, causal)
+    for a, b in zip(got, ref):
+        close(a, b)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_backward_equals_autograd(causal):
+    """Independent derivation: torch autograd of the math attention
+    (the reference test_backward.py:7-18 reference) gives the same gradients."""
+    g = torch.Generator().manual_seed(7)
+    B, H, N, D = 2, 3, 17, 32  # test_backward.py:35-36
+    q, k, v, do = (randn(g, B, H, N, D, dtype=F64) for _ in range(4))
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    s = torch.matmul(qa, ka.transpose(-1, -2)) / D ** 0.5
+    if causal:
+        s = s.masked_fill(torch.triu(torch.ones(N, N, dtype=torch.bool), 1), float("-inf"))
+    o = torch.matmul(torch.softmax(s, -1), va)
+    o.backward(do)
+    out, lse = A.prefill_lse(q, k, v, causal, compute_dtype=F64)
+    close(out, o.detach(), 1e-12)
+    dq, dk, dv = A.backward(do, q, k, v, out, lse, causal)
+    close(dq, qa.grad, 1e-10)
+    close(dk, ka.grad, 1e-10)
+    close(dv, va.grad, 1e-10)
+
+
+def test_backward_finite_differences():
+    """dL/dx for L = sum(dO * O) by central differences on a tiny fp64 case."""
+    g = torch.Generator().manual_seed(3)
+    q, k, v, do = (randn(g, 1, 1, 4, 3, dtype=F64) for _ in range(4))
+
+    def loss(q_, k_, v_):
+        return (A.prefill(q_, k_, v_, True, compute_dtype=F64) * do).sum()
+
+    out, lse = A.prefill_lse(q, k, v, True, compute_dtype=F64)
+    grads = A.backward(do, q, k, v, out, lse, True)
+    eps = 1e-6
+    for which, grad in enumerate(grads):
+        args = [q, k, v]
+        for idx in [(0, 0, 0, 0), (0, 0, 2, 1), (0, 0, 3, 2)]:
+            plus = [a.clone() for a in args]
+            minus = [a.clone() for a in args]
+            plus[which][idx] += eps
+            minus[which][idx] -= eps
+            fd = (loss(*plus) - loss(*minus)) / (2 * eps)
+            assert abs(fd.item() - grad[idx].item()) < 1e-7, (which, idx)
