@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention hot path on the BASELINE configs.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b,7,7b] [--no-cpu]
 
 Prints ONE JSON line.  The headline ``value`` is BASELINE configs[1]: GQA decode
 via forward_decode_gqa_fp16, Q [1,32,1,128], K/V [1,8,4097,128] fp16,
@@ -16,7 +16,8 @@ headline kernel (timed with HIP events on the stream the kernel runs on), and
 ``cpu_baseline``: the CPU oracle (PyTorch eager fp32 math attention with the
 reference's masking, oracle/attention.py) timed on this host on a bounded
 sample of the same workload.  Configs 6a/6b (INT8 KV-cache and sliding-window
-decode) measure the next-row entry points at bandwidth-relevant shapes; they
+decode) measure the next-row entry points at bandwidth-relevant shapes, and
+configs 7/7b the attention backward (fp16 / fp32) at a training shape; they
 are not BASELINE configs.
 """
 from __future__ import annotations
@@ -33,6 +34,7 @@ sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_FP16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA
+MFMA_FP32_PEAK_TFS = 157.3   # MI355X dense fp32 MFMA
 HEADLINE_KERNEL = "decode_splitkv_kernel<128, 4, 0, true>"
 
 
@@ -45,7 +47,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b")
+    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
@@ -289,6 +291,29 @@ def cfg6b_sliding_window(fa, torch, steps, warmup, nsets=3):
                 rotating_sets=nsets), (sets[0], CL, W, S)
 
 
+def cfg7_backward(fa, torch, steps, warmup, dtype="fp16"):
+    """Attention backward (dq, dk, dv) of causal MHA, B=4 H=16 N=2048 D=128, given the
+    forward's out and log-sum-exp.  Algorithmic FLOPs: the five N x N x D products of
+    the backward (S, dP, dV, dK, dQ) over the causal triangle, 2.5x the forward's."""
+    B, H, N, D = 4, 16, 2048, 128
+    dt = torch.float16 if dtype == "fp16" else torch.float32
+    gg = torch.Generator(device="cuda").manual_seed(70)
+    q, k, v, do = [torch.randn(B, H, N, D, generator=gg, device="cuda").to(dt) for _ in range(4)]
+    fwd = fa.forward_fp16_with_lse if dtype == "fp16" else fa.forward_with_lse
+    out, lse = fwd(q, k, v, True)
+    ms = time_gpu(lambda i: fa.backward(do, q, k, v, out, lse, True), steps, warmup)
+    fwd_ms = time_gpu(lambda i: fwd(q, k, v, True), steps, warmup)
+    fwd_flops = 4.0 * B * H * D * N * (N + 1) / 2
+    flops = 2.5 * fwd_flops
+    tfs = flops / (ms * 1e-3) / 1e12
+    peak = MFMA_FP16_PEAK_TFS if dtype == "fp16" else MFMA_FP32_PEAK_TFS
+    return dict(workload=f"backward {dtype} causal B=4 H=16 N=2048 D=128 (dq, dk, dv from out + lse)",
+                ms=ms, tflops=tfs, roofline_frac=tfs / peak, peak_tflops=peak, flops=flops,
+                tokens_per_s=B * N / (ms * 1e-3),
+                forward_with_lse_ms=fwd_ms, forward_with_lse_tflops=fwd_flops / (fwd_ms * 1e-3) / 1e12), \
+        tuple(t[:1, :1].cpu() for t in (do, q, k, v, out, lse))
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_cfg2(torch, sample, budget_s=12.0):
@@ -369,6 +394,14 @@ def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
         by = 2.0 * len(idx) * k.shape[1] * (w + sk) * k.shape[3] * 2
         out["6b"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
                          sample="2 of 16 sequences (the whole cache is read on the CPU)")
+    for c in ("7", "7b"):
+        if c in samples:
+            do, q, k, v, o, lse = samples[c]
+            sec, _ = time_cpu(lambda: A.backward(do, q, k, v, o, lse, True, compute_dtype=torch.float32), budget_s)
+            n, d = q.shape[2], q.shape[3]
+            f = 2.5 * 4.0 * d * n * (n + 1) / 2
+            out[c] = dict(ms=sec * 1e3, tflops=f / sec / 1e12, tokens_per_s=n / sec,
+                          sample="1 of 64 (batch, head) pairs, N=2048, fp32 eager")
     return out
 
 
@@ -410,8 +443,10 @@ def main():
         "5b": lambda: cfg5b_int8(fa, torch, 100, 10),
         "6a": lambda: cfg6a_int8_kv_cache(fa, torch, 100, 10),
         "6b": lambda: cfg6b_sliding_window(fa, torch, 100, 10),
+        "7": lambda: cfg7_backward(fa, torch, 20, 3, "fp16"),
+        "7b": lambda: cfg7_backward(fa, torch, 5, 1, "fp32"),
     }
-    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b"]:
+    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b", "7", "7b"]:
         if c not in want:
             continue
         log(f"config {c} ...")

@@ -27,7 +27,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["decode.hip", "prefill.hip", "train.hip"]
+KERNEL_SOURCES = ["decode.hip", "prefill.hip", "train.hip", "train_fp32.hip"]
 HOST_SOURCES = ["capi.cpp"]
 
 HIP_FLAGS = [
@@ -38,10 +38,11 @@ HIP_FLAGS = [
 ]
 # MFMA accumulators in ordinary VGPRs: without it the compiler parks them in
 # AGPRs and copies them back and forth around every branch of the kernels.
-# The training kernels (train.hip) only accumulate and store their MFMA results,
-# so they keep the accumulators in AGPRs and the VGPRs for operands.
+# The fp32 training kernels (train_fp32.hip) need more operand registers than
+# 256 VGPRs hold, so they keep their accumulators (only ever accumulated and
+# stored) in AGPRs.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
-SOURCE_FLAGS = {"decode.hip": VGPR_FORM, "prefill.hip": VGPR_FORM}
+SOURCE_FLAGS = {"decode.hip": VGPR_FORM, "prefill.hip": VGPR_FORM, "train.hip": VGPR_FORM}
 
 
 def _run(cmd):

@@ -99,59 +99,6 @@ struct PrefillShape {
   static constexpr int WAVES_PER_SIMD = DP <= 64 ? FA_PRE_W64 : (DP <= 128 ? FA_PRE_W128 : 2);  // register budget target
 };
 
-// Physical 16-byte chunk of logical chunk c in tile row r is c ^ chunk_swizzle(r).
-// K reads: 16 lanes read rows 0..15 at one logical chunk -> 16 distinct bank
-// groups.  V transposing reads: 32 lanes read rows 4k..4k+3 at 4 consecutive
-// chunks -> 16 distinct bank groups (rows are 128 B apart for D = 64, so there
-// the row parity also selects the half of the 256-byte bank window).
-template <int DP>
-__device__ __forceinline__ int chunk_swizzle(int r) {
-  if constexpr (DP <= 64)
-    return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-  else
-    return ((r & 3) << 2) | ((r >> 2) & 3);
-}
-
-typedef short short4_t __attribute__((ext_vector_type(4)));
-
-// s_waitcnt vmcnt(N) lgkmcnt(0).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
-}
-
-// One 16-byte-per-lane copy HBM -> LDS (global_load_lds_dwordx4, scalar base +
-// 32-bit lane byte offset): lane i's 16 bytes land at LDS byte address
-// lds_addr + 16 i.  Issued from asm so that the compiler does not track the
-// copy (it would otherwise wait for every copy in flight before the
-// transposing LDS reads); the caller waits with vmcnt before a barrier.  M0,
-// which holds the LDS address, is restored afterwards.
-__device__ __forceinline__ void copy16_to_lds(const half_t* base, unsigned lane_off, unsigned lds_addr) {
-  unsigned saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, %3\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_addr), "v"(lane_off), "s"(base)
-      : "memory");
-}
-
-template <typename T>
-__device__ __forceinline__ const __attribute__((address_space(3))) T* lds_at(unsigned byte_addr) {
-  return reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<size_t>(byte_addr));
-}
-
-// Workgroup barrier that neither waits for outstanding LDS DMA nor lets the
-// compiler move memory operations across it (the caller waits explicitly).
-__device__ __forceinline__ void tile_barrier() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // Varlen output rows that no sequence's attention writes are set to zero by
 // batch + 1 extra workgroups: workgroup b < batch clears rows
 // [cu[b] + min(len_b, row_limit), cu[b+1]) of sequence b, workgroup batch

@@ -68,7 +68,7 @@ int fa_prefill_fp16_lse(const void* q, const void* k, const void* v, void* o,
 
 /*
  * fp32 MHA prefill (fp32 MFMA), optionally with log-sum-exp.
- *   q/k/v/o fp32 [B, H, N, D], 1 <= D <= 128, B*H <= 65535; lse fp32 [B, H, N]
+ *   q/k/v/o fp32 [B, H, N, D], 1 <= D <= 128; lse fp32 [B, H, N]
  *   or NULL.  Causal masks key j > query i.
  * Replaces the launches behind forward (flash_attn_kernel.cu:508-550) and
  * forward_with_lse (:1964-2006), kernel flash_attn_kernel (:369-506).
@@ -87,9 +87,9 @@ size_t fa_backward_workspace_size(int B, int H, int N);
  * and its log-sum-exp `lse` [B, H, N] fp32, writes dq, dk, dv (same shape and
  * type as q).  fp16 variant: every tensor but lse is fp16 (gradients
  * accumulate in fp32 and are rounded once); fp32 variant: all fp32.
- * 1 <= D <= 128, B*H <= 65535.  Two launches on `stream` (dQ with the row
- * statistic delta = rowsum(dout * out) into the workspace, then dK/dV);
- * deterministic (no atomics).  The workspace needs no initialisation.
+ * 1 <= D <= 128.  Two or three launches on `stream` (dQ with the row
+ * statistic delta = rowsum(dout * out) into the workspace, then dK/dV, as one
+ * pass or as a dV and a dK pass); deterministic (no atomics).  The workspace needs no initialisation.
  * Replaces flash_attn_backward (flash_attn_kernel.cu:2173-2264), kernels
  * flash_attn_backward_tiled_kernel_fp32/_fp16 (:2056-2171).
  */
