@@ -385,32 +385,57 @@ inline int train_grid(const TrainParams& p) {
   return p.BH >= 8 ? 8 * ceil_div(p.BH, 8) * p.nblk : p.BH * p.nblk;
 }
 
-// Drives a TileRing over `ntiles` tiles starting at row r_first: calls
-// compute(stage, tile) once per tile with the tile resident in `stage`.
+// Drives a TileRing over `ntiles` tiles starting at row r_first and calls
+// compute(stage, tile) for the tiles [c_begin, c_end) of this wave (every wave
+// copies and joins the barriers of all tiles).  The three tile ranges are
+// separate loops so that the accumulating loop carries no per-tile branch
+// around the MFMAs (which would make the compiler copy the accumulators).
 template <typename Ring, bool DMA, bool VEC, typename T, typename Compute>
 __device__ __forceinline__ void run_ring(Ring& ring, const T* pa, const T* pb, const float* va, const float* vb,
-                                         int r_first, int ntiles, int rows, int d, Compute&& compute) {
+                                         int r_first, int ntiles, int c_begin, int c_end, int rows, int d,
+                                         Compute&& compute) {
+  c_begin = max(0, min(c_begin, ntiles));
+  c_end = max(c_begin, min(c_end, ntiles));
   if constexpr (DMA) {
     constexpr int NS = Ring::NS;
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
       if (s < ntiles) ring.dma(pa, pb, va, vb, r_first + s * kRows, rows, d, s);
-    for (int t = 0; t < ntiles; ++t) {
+    auto step = [&](int t) {
       ring.wait_dma(t + 1 < ntiles);  // this wave's copies of tile t landed
       tile_barrier();                  // everyone's did; stage (t - 1) % NS is free
       if (t + NS - 1 < ntiles) ring.dma(pa, pb, va, vb, r_first + (t + NS - 1) * kRows, rows, d, (t + NS - 1) % NS);
+    };
+    for (int t = 0; t < c_begin; ++t) step(t);
+    for (int t = c_begin; t < c_end; ++t) {
+      step(t);
       compute(t % NS, t);
     }
+    for (int t = c_end; t < ntiles; ++t) step(t);
   } else {
     if (ntiles > 0) {
       ring.template load<VEC>(pa, pb, va, vb, r_first, rows, d);
       ring.store(0);
     }
-    for (int t = 0; t < ntiles; ++t) {
+    auto pre = [&](int t) {
       if (t + 1 < ntiles) ring.template load<VEC>(pa, pb, va, vb, r_first + (t + 1) * kRows, rows, d);
       __syncthreads();
-      compute(t & 1, t);
+    };
+    auto post = [&](int t) {
       if (t + 1 < ntiles) ring.store((t + 1) & 1);
+    };
+    for (int t = 0; t < c_begin; ++t) {
+      pre(t);
+      post(t);
+    }
+    for (int t = c_begin; t < c_end; ++t) {
+      pre(t);
+      compute(t & 1, t);
+      post(t);
+    }
+    for (int t = c_end; t < ntiles; ++t) {
+      pre(t);
+      post(t);
     }
   }
 }
@@ -485,9 +510,10 @@ __global__ __launch_bounds__(kThreads) void query_major_kernel(TrainParams p) {
 
   Ring ring(smem, tid, D);
   const Reader<T, DP> rd(lane);
-  run_ring<Ring, DMA, VEC>(ring, kp, vp, nullptr, nullptr, 0, ntiles, N, D, [&](int stage, int t) {
+  // this wave computes key tiles [0, ceil(kend_w / 32)): later ones are past its diagonal
+  run_ring<Ring, DMA, VEC>(ring, kp, vp, nullptr, nullptr, 0, ntiles, 0, (kend_w + kRows - 1) / kRows, N, D,
+                           [&](int stage, int t) {
     const int kt = t * kRows;
-    if (kt >= kend_w) return;  // past this wave's diagonal
     const unsigned ks = ring.addr_a(stage);
     const unsigned vs = ring.addr_b(stage);
     // S^T = K Q^T: lane <-> query, register r <-> key kt + 8 (r/4) + 4 hi + r%4
@@ -624,10 +650,11 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(TrainParams p) {
 
   Ring ring(smem, tid, D);
   const Reader<T, DP> rd(lane);
-  run_ring<Ring, DMA, VEC>(ring, qp, dop, lse, dlt, qstart, ntiles, N, D, [&](int stage, int t) {
+  // a tile whose last query precedes this wave's first key contributes nothing:
+  // causal waves start at the tile holding query wk0
+  const int c_begin = p.causal ? (wk0 - qstart) / kRows : 0;
+  run_ring<Ring, DMA, VEC>(ring, qp, dop, lse, dlt, qstart, ntiles, c_begin, ntiles, N, D, [&](int stage, int t) {
     const int qt = qstart + t * kRows;
-    // a tile whose last query precedes this wave's first key contributes nothing
-    if (p.causal && qt + kRows - 1 < wk0) return;
     const unsigned qs = ring.addr_a(stage);
     const unsigned ds = ring.addr_b(stage);
     // S = Q K^T and dP = dO V^T: lane <-> key, register r <-> query qt + 8 (r/4) + 4 hi + r%4
