@@ -142,3 +142,63 @@ def test_capi_decode_prefill_on_gpu(lib):
     assert rc == FA_OK, lib.fa_last_error()
     torch.cuda.synchronize()
     assert_close(o, A.prefill(q, k, v, True), what="capi prefill")
+
+
+def test_training_argument_errors_without_a_gpu(lib):
+    null = _vp()
+    lib.fa_backward_workspace_size.restype = ctypes.c_size_t
+    lib.fa_backward_workspace_size.argtypes = [ctypes.c_int] * 3
+    assert lib.fa_backward_workspace_size(2, 3, 17) == 2 * 3 * 17 * 4
+    assert lib.fa_backward_workspace_size(0, 3, 17) == 0
+    # D above 128
+    rc = lib.fa_prefill_fp32(null, null, null, null, null, 1, 2, 16, 160, 1, null)
+    assert rc == FA_ERR_UNSUPPORTED
+    rc = lib.fa_backward_fp16(null, null, null, null, null, null, null, null, null, 1, 2, 16, 160, 1, null,
+                              ctypes.c_size_t(0), null)
+    assert rc == FA_ERR_UNSUPPORTED
+    # null pointers / missing workspace
+    rc = lib.fa_prefill_fp16_lse(_vp(16), _vp(16), _vp(16), _vp(16), null, 1, 2, 16, 64, 1, null)
+    assert rc == FA_ERR_INVALID_ARG
+    p = _vp(16)
+    rc = lib.fa_backward_fp32(p, p, p, p, p, p, p, p, p, 1, 2, 16, 64, 1, null, ctypes.c_size_t(0), null)
+    assert rc == FA_ERR_WORKSPACE
+    # empty problems are no-ops
+    assert lib.fa_backward_fp16(null, null, null, null, null, null, null, null, null, 0, 2, 16, 64, 1, null,
+                                ctypes.c_size_t(0), null) == FA_OK
+
+
+@pytest.mark.gpu
+def test_capi_training_on_gpu(lib):
+    """fa_prefill_fp32 (with LSE), fa_prefill_fp16_lse and fa_backward_fp16 through ctypes."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    g = torch.Generator().manual_seed(1)
+    B, H, N, D = 1, 2, 100, 64
+    q, k, v, do = (randn(g, B, H, N, D) for _ in range(4))
+    qc, kc, vc, dc = (t.cuda() for t in (q, k, v, do))
+    # fp32 forward + LSE
+    q32, k32, v32 = (t.float().contiguous() for t in (qc, kc, vc))
+    o32 = torch.empty_like(q32)
+    l32 = torch.empty(B, H, N, device="cuda")
+    rc = lib.fa_prefill_fp32(_p(q32), _p(k32), _p(v32), _p(o32), _p(l32), B, H, N, D, 1, st)
+    assert rc == FA_OK, lib.fa_last_error()
+    ro, rl = A.prefill_lse(q.float(), k.float(), v.float(), True, compute_dtype=torch.float64)
+    torch.cuda.synchronize()
+    assert_close(o32, ro, atol=2e-4, rtol=2e-4, what="capi fp32 forward")
+    assert_close(l32, rl, atol=2e-4, rtol=2e-4, what="capi fp32 lse")
+    # fp16 forward + LSE, then backward
+    o = torch.empty_like(qc)
+    lse = torch.empty(B, H, N, device="cuda")
+    rc = lib.fa_prefill_fp16_lse(_p(qc), _p(kc), _p(vc), _p(o), _p(lse), B, H, N, D, 1, st)
+    assert rc == FA_OK, lib.fa_last_error()
+    nbytes = lib.fa_backward_workspace_size(B, H, N)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dq, dk, dv = (torch.empty_like(qc) for _ in range(3))
+    rc = lib.fa_backward_fp16(_p(dc), _p(qc), _p(kc), _p(vc), _p(o), _p(lse), _p(dq), _p(dk), _p(dv),
+                              B, H, N, D, 1, _p(ws), ctypes.c_size_t(nbytes), st)
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    ref = A.backward(do, q, k, v, o.cpu(), lse.cpu(), True)
+    for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
+        assert_close(a, r, atol=3e-2, rtol=3e-2, what=f"capi backward {name}")
