@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention hot path on the BASELINE configs.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b,7,7b] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b,7,7b,8] [--no-cpu]
 
 Prints ONE JSON line.  The headline ``value`` is BASELINE configs[1]: GQA decode
 via forward_decode_gqa_fp16, Q [1,32,1,128], K/V [1,8,4097,128] fp16,
@@ -17,8 +17,8 @@ headline kernel (timed with HIP events on the stream the kernel runs on), and
 reference's masking, oracle/attention.py) timed on this host on a bounded
 sample of the same workload.  Configs 6a/6b (INT8 KV-cache and sliding-window
 decode) measure the next-row entry points at bandwidth-relevant shapes, and
-configs 7/7b the attention backward (fp16 / fp32) at a training shape; they
-are not BASELINE configs.
+configs 7/7b the attention backward (fp16 / fp32) at a training shape, and
+config 8 KV-cache token eviction; they are not BASELINE configs.
 """
 from __future__ import annotations
 
@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b")
+    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b,8")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
@@ -314,6 +314,28 @@ def cfg7_backward(fa, torch, steps, warmup, dtype="fp16"):
         tuple(t[:1, :1].cpu() for t in (do, q, k, v, out, lse))
 
 
+def cfg8_token_eviction(fa, torch, steps, warmup, nsets=3):
+    """token_eviction: B=16, 8 KV heads, N=1024 (the reference's limit), D=128,
+    evicting 256 tokens per row.  Algorithmic bytes: kept K/V rows read once,
+    every K/V output row written once, scores read, mask written."""
+    B, H, N, D, E = 16, 8, 1024, 128, 256
+    gg = torch.Generator(device="cuda").manual_seed(80)
+    sets = [(torch.randn(B, H, N, D, generator=gg, device="cuda").half(),
+             torch.randn(B, H, N, D, generator=gg, device="cuda").half(),
+             torch.randn(B, N, generator=gg, device="cuda")) for _ in range(nsets)]
+
+    def step(i):
+        k, v, sc = sets[i % nsets]
+        fa.token_eviction(k, v, sc, E)
+
+    ms = time_gpu(step, steps, warmup)
+    total = 2.0 * B * H * (N - E) * D * 2 + 2.0 * B * H * N * D * 2 + 4.0 * B * N * 2
+    gbs = total / (ms * 1e-3) / 1e9
+    return dict(workload="token_eviction B=16 H_KV=8 N=1024 D=128 num_evict=256",
+                ms=ms, gbs=gbs, roofline_frac=gbs / HBM_PEAK_GBS, bytes=total, rotating_sets=nsets,
+                tokens_per_s=B * N / (ms * 1e-3)), tuple(t[:2].cpu() for t in sets[0]) + (E,)
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_cfg2(torch, sample, budget_s=12.0):
@@ -394,6 +416,12 @@ def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
         by = 2.0 * len(idx) * k.shape[1] * (w + sk) * k.shape[3] * 2
         out["6b"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=len(idx) / sec,
                          sample="2 of 16 sequences (the whole cache is read on the CPU)")
+    if "8" in samples:
+        k, v, sc, e = samples["8"]
+        sec, _ = time_cpu(lambda: A.token_eviction(k, v, sc, e), budget_s)
+        by = 2.0 * k.shape[0] * k.shape[1] * (k.shape[2] - e) * k.shape[3] * 2 + 2.0 * k.numel() * 2
+        out["8"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=k.shape[0] * k.shape[2] / sec,
+                        sample="2 of 16 batch rows")
     for c in ("7", "7b"):
         if c in samples:
             do, q, k, v, o, lse = samples[c]
@@ -445,8 +473,9 @@ def main():
         "6b": lambda: cfg6b_sliding_window(fa, torch, 100, 10),
         "7": lambda: cfg7_backward(fa, torch, 20, 3, "fp16"),
         "7b": lambda: cfg7_backward(fa, torch, 5, 1, "fp32"),
+        "8": lambda: cfg8_token_eviction(fa, torch, 100, 10),
     }
-    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b", "7", "7b"]:
+    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b", "7", "7b", "8"]:
         if c not in want:
             continue
         log(f"config {c} ...")

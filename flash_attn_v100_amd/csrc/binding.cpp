@@ -594,6 +594,34 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> backward(at::Tensor dout, at::Ten
   return std::make_tuple(dq, dk, dv);
 }
 
+// token_eviction (flash_attn_kernel.cu:4296-4344): (k_out, v_out, valid_mask).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> token_eviction(at::Tensor k, at::Tensor v, at::Tensor attn_scores,
+                                                              int num_evict) {
+  CHECK_INPUT(k);
+  CHECK_INPUT(v);
+  CHECK_INPUT(attn_scores);
+  TORCH_CHECK(k.dtype() == at::kHalf, "k must be float16");
+  TORCH_CHECK(v.dtype() == at::kHalf, "v must be float16");
+  TORCH_CHECK(attn_scores.dtype() == at::kFloat, "attn_scores must be float32");
+  CHECK_DIM(k, 4);
+  TORCH_CHECK(v.sizes() == k.sizes(), "k and v must have the same shape");
+  CHECK_SAME_DEVICE(k, v);
+  CHECK_SAME_DEVICE(k, attn_scores);
+  const auto B = k.size(0), H = k.size(1), N = k.size(2), D = k.size(3);
+  CHECK_DIM(attn_scores, 2);
+  TORCH_CHECK(attn_scores.size(0) == B, "attn_scores batch mismatch");
+  TORCH_CHECK(attn_scores.size(1) == N, "attn_scores length mismatch");
+  TORCH_CHECK(N <= 1024, "N must be <= 1024 for token eviction");
+  HIPGuardMasqueradingAsCUDA guard(k.device());
+  auto k_out = at::empty_like(k);
+  auto v_out = at::empty_like(v);
+  auto mask = at::empty({B, N}, k.options().dtype(at::kInt));
+  check_fa(fa_token_eviction(k.data_ptr(), v.data_ptr(), attn_scores.data_ptr<float>(), k_out.data_ptr(),
+                             v_out.data_ptr(), mask.data_ptr<int32_t>(), to_int(B, "B"), to_int(H, "H_KV"),
+                             to_int(N, "N"), to_int(D, "D"), num_evict, cur_stream()));
+  return std::make_tuple(k_out, v_out, mask);
+}
+
 // ---------------------------------------------------------------------------
 // Names of the reference module that are outside the MI355X hot path.
 
@@ -790,7 +818,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_with_lse", &forward_with_lse, "fp32 forward with logsumexp (MI355X)");
   m.def("forward_fp16_with_lse", &forward_fp16_with_lse, "fp16 forward with logsumexp (MI355X MFMA)");
   m.def("backward", &backward, "Attention backward for MHA, fp32/fp16 (MI355X MFMA)");
-  for (const char* name : {"speculative_verify", "token_eviction",
+  m.def("token_eviction", &token_eviction, "KV-cache token eviction by attention score (MI355X)");
+  for (const char* name : {"speculative_verify",
                            "cross_gpu_allreduce_fp16", "scatter_heads",
                            "gather_heads"}) {
     std::string n(name);

@@ -218,6 +218,22 @@ int fa_decode_int8_gqa(const void* q, const void* k, const void* v, void* o,
                        int H_Q, int H_KV, int N, int D, int cache_len,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * KV-cache token eviction.  Per batch row b, the num_evict tokens with the
+ * lowest attn_scores[b, :] (ties: lower index first, i.e. a stable ascending
+ * sort) are dropped; the kept K/V rows of every KV head are written, in their
+ * original order, to the front of k_out/v_out and the remaining rows are
+ * zero.  keep_mask int32 [B, N] receives 1 for kept and 0 for evicted tokens.
+ *   k/v/k_out/v_out fp16 [B, H_KV, N, D], attn_scores fp32 [B, N], N <= 1024;
+ *   num_evict <= 0 keeps all, >= N drops all.  Scores with NaN are outside
+ *   the contract.  Two launches on `stream`.
+ * Replaces token_eviction_forward (flash_attn_kernel.cu:4296-4344), kernel
+ * token_eviction_kernel (:4223-4294).
+ */
+int fa_token_eviction(const void* k, const void* v, const float* attn_scores,
+                      void* k_out, void* v_out, int32_t* keep_mask, int B,
+                      int H_KV, int N, int D, int num_evict, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -394,3 +394,27 @@ def backward(dout, q, k, v, out, lse, causal: bool, compute_dtype=torch.float64)
     dk = torch.matmul(ds.transpose(-1, -2), qf)
     dv = torch.matmul(p.transpose(-1, -2), dof)
     return dq, dk, dv
+
+
+def token_eviction(k, v, attn_scores, num_evict: int):
+    """``token_eviction`` (flash_attn_kernel.cu:4223-4344).
+
+    Per batch row, the reference bubble-sorts the scores ascending, swapping
+    only on ``s[j] > s[j+1]`` (:4258-4270, a stable sort), marks the first
+    ``num_evict`` sorted tokens evicted (:4272-4277), and copies the kept K/V
+    rows of every head, in order, to the front of zero-filled outputs
+    (:4281-4293; outputs are ``zeros_like``, :4317-4318).  Returns
+    ``(k_out, v_out, valid_mask)`` with valid_mask int32 [B, N].
+    """
+    B, H, N, D = k.shape
+    order = torch.sort(attn_scores, dim=1, stable=True).indices
+    mask = torch.ones(B, N, dtype=torch.int32)
+    ne = max(0, min(int(num_evict), N))
+    k_out = torch.zeros_like(k)
+    v_out = torch.zeros_like(v)
+    for b in range(B):
+        mask[b, order[b, :ne]] = 0
+        kept = torch.nonzero(mask[b], as_tuple=False).flatten()
+        k_out[b, :, :kept.numel()] = k[b, :, kept]
+        v_out[b, :, :kept.numel()] = v[b, :, kept]
+    return k_out, v_out, mask

@@ -336,3 +336,37 @@ def backward(dout, q, k, v, out, lse, causal):
                         dk[b][h][j][t] += ds * qi[t]
                         dv[b][h][j][t] += p * doi[t]
     return dq, dk, dv
+
+
+def token_eviction(k, v, attn_scores, num_evict):
+    """token_eviction_kernel (flash_attn_kernel.cu:4223-4294) as written: the
+    one-thread bubble sort (swap on s[j] > s[j+1]), the mask of the first
+    num_evict sorted indices, and the in-order copy of kept rows.  Returns
+    nested lists (k_out, v_out, mask)."""
+    k, v, sc = _tolist(k), _tolist(v), _tolist(attn_scores)
+    B, H, N, D = len(k), len(k[0]), len(k[0][0]), len(k[0][0][0])
+    k_out = [[[[0.0] * D for _ in range(N)] for _ in range(H)] for _ in range(B)]
+    v_out = [[[[0.0] * D for _ in range(N)] for _ in range(H)] for _ in range(B)]
+    masks = []
+    for b in range(B):
+        s = list(sc[b])
+        idx = list(range(N))
+        for i in range(N - 1):
+            for j in range(N - 1 - i):
+                if s[j] > s[j + 1]:
+                    s[j], s[j + 1] = s[j + 1], s[j]
+                    idx[j], idx[j + 1] = idx[j + 1], idx[j]
+        mask = [1] * N
+        i = 0
+        while i < num_evict and i < N:
+            mask[idx[i]] = 0
+            i += 1
+        masks.append(mask)
+        for h in range(H):
+            w = 0
+            for i in range(N):
+                if mask[i]:
+                    k_out[b][h][w] = list(k[b][h][i])
+                    v_out[b][h][w] = list(v[b][h][i])
+                    w += 1
+    return k_out, v_out, masks

@@ -417,3 +417,30 @@ def test_backward_finite_differences():
             minus[which][idx] -= eps
             fd = (loss(*plus) - loss(*minus)) / (2 * eps)
             assert abs(fd.item() - grad[idx].item()) < 1e-7, (which, idx)
+
+
+# ---------------------------------------------------------------- token eviction
+
+@pytest.mark.parametrize("n,num_evict", [(1, 0), (1, 1), (7, 3), (16, 0), (16, 16), (16, 20), (33, -2), (40, 11)])
+def test_token_eviction_vs_brute(n, num_evict):
+    g = torch.Generator().manual_seed(n * 31 + num_evict)
+    k = randn(g, 2, 3, n, 4)
+    v = randn(g, 2, 3, n, 4)
+    # few distinct values: many ties, so the stable tie order is exercised
+    sc = torch.randint(0, 5, (2, n), generator=g).float() * 0.5
+    ko, vo, m = A.token_eviction(k, v, sc, num_evict)
+    bk, bv, bm = Bt.token_eviction(k, v, sc, num_evict)
+    assert torch.equal(m, torch.tensor(bm, dtype=torch.int32))
+    assert torch.equal(ko, torch.tensor(bk, dtype=torch.float16))
+    assert torch.equal(vo, torch.tensor(bv, dtype=torch.float16))
+
+
+def test_token_eviction_closed_forms():
+    g = torch.Generator().manual_seed(9)
+    k, v = randn(g, 1, 2, 10, 8), randn(g, 1, 2, 10, 8)
+    sc = torch.arange(10, dtype=torch.float32).flip(0).unsqueeze(0)  # token 9 lowest
+    ko, vo, m = A.token_eviction(k, v, sc, 3)
+    assert m.tolist() == [[1] * 7 + [0] * 3]  # the three lowest scores are tokens 7, 8, 9
+    assert torch.equal(ko[:, :, :7], k[:, :, :7]) and not ko[:, :, 7:].any()
+    ko, vo, m = A.token_eviction(k, v, sc, 0)
+    assert torch.equal(ko, k) and torch.equal(vo, v) and bool(m.all())
