@@ -1,6 +1,6 @@
 """Benchmark of the MI355X attention hot path on the BASELINE configs.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b,7,7b,8] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5a,5b,6a,6b,7,7b,8,9] [--no-cpu]
 
 Prints ONE JSON line.  The headline ``value`` is BASELINE configs[1]: GQA decode
 via forward_decode_gqa_fp16, Q [1,32,1,128], K/V [1,8,4097,128] fp16,
@@ -18,7 +18,8 @@ reference's masking, oracle/attention.py) timed on this host on a bounded
 sample of the same workload.  Configs 6a/6b (INT8 KV-cache and sliding-window
 decode) measure the next-row entry points at bandwidth-relevant shapes, and
 configs 7/7b the attention backward (fp16 / fp32) at a training shape, and
-config 8 KV-cache token eviction; they are not BASELINE configs.
+config 8 KV-cache token eviction, config 9 speculative verification; they
+are not BASELINE configs.
 """
 from __future__ import annotations
 
@@ -47,7 +48,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b,8")
+    ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b,8,9")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
@@ -336,6 +337,24 @@ def cfg8_token_eviction(fa, torch, steps, warmup, nsets=3):
                 tokens_per_s=B * N / (ms * 1e-3)), tuple(t[:2].cpu() for t in sets[0]) + (E,)
 
 
+def cfg9_speculative_verify(fa, torch, steps, warmup):
+    """speculative_verify: B=16 rows, K=4 draft tokens, vocabulary 32000 (the
+    reference test's large case).  Independent random target/draft
+    distributions, so most rows reject early and run the full residual scans.
+    Latency-bound: each sampled index comes from a serial fp32 running sum."""
+    B, K, V = 16, 4, 32000
+    gg = torch.Generator(device="cuda").manual_seed(90)
+    tp = torch.softmax(torch.randn(B, K + 1, V, generator=gg, device="cuda"), -1)
+    dp = torch.softmax(torch.randn(B, K, V, generator=gg, device="cuda"), -1)
+    tok = torch.randint(0, V, (B, K), generator=gg, device="cuda")
+    rv = torch.rand(B, K, generator=gg, device="cuda")
+    ms = time_gpu(lambda i: fa.speculative_verify(tp, dp, tok, rv, K), steps, warmup)
+    acc, _ = fa.speculative_verify(tp, dp, tok, rv, K)
+    return dict(workload="speculative_verify B=16 K=4 vocab=32000", ms=ms, us_per_call=ms * 1e3,
+                rows_per_s=B / (ms * 1e-3), mean_accepted=float(acc.float().mean().item()),
+                bound="serial fp32 running sums (latency)"), (tp[:2].cpu(), dp[:2].cpu(), tok[:2].cpu(), rv[:2].cpu(), K)
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_cfg2(torch, sample, budget_s=12.0):
@@ -422,6 +441,10 @@ def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
         by = 2.0 * k.shape[0] * k.shape[1] * (k.shape[2] - e) * k.shape[3] * 2 + 2.0 * k.numel() * 2
         out["8"] = dict(ms=sec * 1e3, gbs=by / sec / 1e9, tokens_per_s=k.shape[0] * k.shape[2] / sec,
                         sample="2 of 16 batch rows")
+    if "9" in samples:
+        tp, dp, tok, rv, kk = samples["9"]
+        sec, _ = time_cpu(lambda: A.speculative_verify(tp, dp, tok, rv, kk), budget_s)
+        out["9"] = dict(ms=sec * 1e3, rows_per_s=tp.shape[0] / sec, sample="2 of 16 batch rows (numpy float32)")
     for c in ("7", "7b"):
         if c in samples:
             do, q, k, v, o, lse = samples[c]
@@ -474,8 +497,9 @@ def main():
         "7": lambda: cfg7_backward(fa, torch, 20, 3, "fp16"),
         "7b": lambda: cfg7_backward(fa, torch, 5, 1, "fp32"),
         "8": lambda: cfg8_token_eviction(fa, torch, 100, 10),
+        "9": lambda: cfg9_speculative_verify(fa, torch, 50, 5),
     }
-    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b", "7", "7b", "8"]:
+    for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b", "7", "7b", "8", "9"]:
         if c not in want:
             continue
         log(f"config {c} ...")

@@ -622,6 +622,42 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> token_eviction(at::Tensor k, at::
   return std::make_tuple(k_out, v_out, mask);
 }
 
+// speculative_verify (flash_attn_kernel.cu:3972-4018): (accepted_count, output_tokens).
+std::tuple<at::Tensor, at::Tensor> speculative_verify(at::Tensor target_probs, at::Tensor draft_probs,
+                                                      at::Tensor draft_tokens, at::Tensor random_vals, int K) {
+  CHECK_INPUT(target_probs);
+  CHECK_INPUT(draft_probs);
+  CHECK_INPUT(draft_tokens);
+  CHECK_INPUT(random_vals);
+  TORCH_CHECK(target_probs.dtype() == at::kFloat, "target_probs must be float32");
+  TORCH_CHECK(draft_probs.dtype() == at::kFloat, "draft_probs must be float32");
+  TORCH_CHECK(draft_tokens.dtype() == at::kLong, "draft_tokens must be int64");
+  TORCH_CHECK(random_vals.dtype() == at::kFloat, "random_vals must be float32");
+  CHECK_DIM(target_probs, 3);
+  const auto B = target_probs.size(0), V = target_probs.size(2);
+  TORCH_CHECK(K <= 8, "K must be <= SPEC_MAX_K(8)");
+  TORCH_CHECK(K >= 1, "K must be >= 1");
+  TORCH_CHECK(target_probs.size(1) == K + 1, "target_probs must have K+1 positions");
+  CHECK_DIM(draft_probs, 3);
+  TORCH_CHECK(draft_probs.size(0) == B && draft_probs.size(2) == V, "draft_probs must be [B, K, vocab_size]");
+  TORCH_CHECK(draft_probs.size(1) == K, "draft_probs must have K positions");
+  CHECK_DIM(draft_tokens, 2);
+  TORCH_CHECK(draft_tokens.size(0) == B, "draft_tokens batch mismatch");
+  TORCH_CHECK(draft_tokens.size(1) == K, "draft_tokens must have K tokens");
+  TORCH_CHECK(random_vals.numel() >= B * K, "random_vals must hold B*K values");
+  CHECK_SAME_DEVICE(target_probs, draft_probs);
+  CHECK_SAME_DEVICE(target_probs, draft_tokens);
+  CHECK_SAME_DEVICE(target_probs, random_vals);
+  HIPGuardMasqueradingAsCUDA guard(target_probs.device());
+  auto accepted = at::empty({B}, target_probs.options().dtype(at::kInt));
+  auto tokens = at::empty({B, K + 1}, target_probs.options().dtype(at::kLong));
+  check_fa(fa_speculative_verify(target_probs.data_ptr<float>(), draft_probs.data_ptr<float>(),
+                                 draft_tokens.data_ptr<int64_t>(), random_vals.data_ptr<float>(),
+                                 accepted.data_ptr<int32_t>(), tokens.data_ptr<int64_t>(), to_int(B, "B"), K,
+                                 to_int(V, "vocab_size"), cur_stream()));
+  return std::make_tuple(accepted, tokens);
+}
+
 // ---------------------------------------------------------------------------
 // Names of the reference module that are outside the MI355X hot path.
 
@@ -819,8 +855,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_fp16_with_lse", &forward_fp16_with_lse, "fp16 forward with logsumexp (MI355X MFMA)");
   m.def("backward", &backward, "Attention backward for MHA, fp32/fp16 (MI355X MFMA)");
   m.def("token_eviction", &token_eviction, "KV-cache token eviction by attention score (MI355X)");
-  for (const char* name : {"speculative_verify",
-                           "cross_gpu_allreduce_fp16", "scatter_heads",
+  m.def("speculative_verify", &speculative_verify, "Speculative decoding verify (MI355X)");
+  for (const char* name : {"cross_gpu_allreduce_fp16", "scatter_heads",
                            "gather_heads"}) {
     std::string n(name);
     m.def(name, [n](pybind11::args, pybind11::kwargs) { not_implemented(n.c_str()); }, "Not implemented on MI355X");

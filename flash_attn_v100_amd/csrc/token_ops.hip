@@ -1,5 +1,6 @@
-// KV-cache token eviction for gfx950.
+// KV-cache token eviction and speculative-decoding verification for gfx950.
 //
+// ---- token eviction ----
 // The reference (flash_attn_kernel.cu:4223-4344) bubble-sorts each batch
 // row's attention scores ascending on one thread (swapping only when
 // s[j] > s[j+1], i.e. a stable sort), evicts the `num_evict` lowest, and
@@ -144,6 +145,204 @@ __global__ __launch_bounds__(kThreads) void compact_kernel(const half_t* __restr
 }
 
 }  // namespace evict
+
+// ---- speculative verification ----
+// The reference (flash_attn_kernel.cu:3853-4018) accepts draft token t at
+// step i when r_i < min(1, p_t / (q_t + 1e-10)); at the first rejection it
+// samples from max(target - draft, 0) / Z and draws a bonus token from the
+// next target row, each by a running fp32 sum over the vocabulary compared
+// against r (with its "tok == 0" update rule: a hit at index 0 is replaced by
+// the next hit).  The sampled indices depend on the exact fp32 value of every
+// partial sum, so each sum is accumulated serially in index order, as there.
+// One workgroup of two waves per batch row: wave 0 computes Z and then the
+// residual sample, wave 1 the bonus token, concurrently.  Within a wave the 64
+// lanes load 256 consecutive elements and compute their terms (differences,
+// the division by Z) in parallel into LDS, with the next 256 already loading;
+// lane 0 then runs only the dependent adds, every lane tests the running sums,
+// and the sample and bonus scans stop at their first decisive hit.
+namespace spec {
+
+constexpr int kMaxK = 8;     // SPEC_MAX_K (flash_attn_kernel.cu:3851)
+constexpr int kChunk = 256;  // elements per wave step (4 per lane)
+
+enum ChainMode { kZ = 0, kResidual = 1, kPrefix = 2, kBonus = 3 };
+
+// Serial scan of row a (minus row b for kZ / kResidual) over [0, V).
+//  kZ:        *sum = the sum of the positive (a - b) in index order.
+//  kResidual: cs += (a - b) / Z where a - b > 0; hit at such v when r < cs.
+//  kPrefix:   cs += a; hit when r < cs.
+//  kBonus:    cs += a; hit when cs >= r.
+// Returns the reference's token: the first hit, or the next hit if the first
+// is index 0 (0 without hits).  Per 256-element chunk: every lane computes 4
+// terms into LDS (a term that does not contribute is -0.0, which leaves a
+// non-negative running sum unchanged, so the chain needs no test); lane 0
+// runs the dependent adds over them, 64 at a time in registers, writing the
+// running sums back; then every lane tests 4 of them and a ballot finds the
+// first hit.  For kResidual the first v with r < cs always contributed (cs
+// only grows where a term is added); a later hit must contribute too.
+template <int MODE>
+__device__ int chain(const float* __restrict__ a, const float* __restrict__ b, int V, float Z, float r, float* sum,
+                     float* lds) {
+  const int lane = threadIdx.x & 63;
+  float cs = 0.0f;  // lane 0's running sum
+  int tok = 0;
+  bool zero_hit = false;  // a hit at index 0 was seen: the next hit decides
+  auto load = [&](int c0, float (&x)[4], float (&y)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int v = c0 + 4 * lane + e;
+      x[e] = v < V ? a[v] : 0.0f;
+      if constexpr (MODE == kZ || MODE == kResidual) y[e] = v < V ? b[v] : 0.0f;
+    }
+  };
+  float xa[4], ya[4], xn[4], yn[4];
+  load(0, xn, yn);
+  for (int c0 = 0; c0 < V; c0 += kChunk) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      xa[e] = xn[e];
+      ya[e] = yn[e];
+    }
+    if (c0 + kChunk < V) load(c0 + kChunk, xn, yn);
+    bool contrib[4];
+    float4_t t4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float t;
+      if constexpr (MODE == kZ || MODE == kResidual) {
+        const float d = xa[e] - ya[e];
+        contrib[e] = d > 0.0f;
+        t = contrib[e] ? (MODE == kZ ? d : d / Z) : -0.0f;
+      } else {
+        contrib[e] = true;
+        t = xa[e];
+      }
+      // elements past V add -0.0 (no change) and never hit
+      if (c0 + 4 * lane + e >= V) {
+        t = -0.0f;
+        contrib[e] = false;
+      }
+      t4[e] = t;
+    }
+    *reinterpret_cast<float4_t*>(lds + 4 * lane) = t4;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < kChunk; h += 64) {
+        float4_t q[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) q[j] = *reinterpret_cast<const float4_t*>(lds + h + 4 * j);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            cs += q[j][e];
+            q[j][e] = cs;
+          }
+        if constexpr (MODE != kZ)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) *reinterpret_cast<float4_t*>(lds + h + 4 * j) = q[j];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    if constexpr (MODE != kZ) {
+      const float4_t c4 = *reinterpret_cast<const float4_t*>(lds + 4 * lane);
+      int best = -1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const bool hit = (MODE == kBonus) ? (c4[e] >= r) : (r < c4[e]) && contrib[e];
+        const int v = c0 + 4 * lane + e;
+        // after a hit at index 0 only later hits (v > 0) count
+        const bool ok = hit && !(v == 0 && zero_hit);
+        if (ok && best < 0) best = v;
+      }
+      // lowest v with a hit across the wave: lanes are ordered, so the first lane with a hit wins
+      const unsigned long long m = __builtin_amdgcn_ballot_w64(best >= 0);
+      if (m != 0) {
+        const int src = __builtin_ctzll(m);
+        const int v0 = __builtin_amdgcn_readlane(best, src);
+        if (v0 != 0) {
+          tok = v0;
+          break;
+        }
+        // the hit is index 0: remember it and look for the next one
+        zero_hit = true;
+        int best2 = -1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = c0 + 4 * lane + e;
+          const bool hit = (MODE == kBonus) ? (c4[e] >= r) : (r < c4[e]) && contrib[e];
+          if (hit && v > 0 && best2 < 0) best2 = v;
+        }
+        const unsigned long long m2 = __builtin_amdgcn_ballot_w64(best2 >= 0);
+        if (m2 != 0) {
+          tok = __builtin_amdgcn_readlane(best2, __builtin_ctzll(m2));
+          break;
+        }
+      }
+    }
+  }
+  if (sum) *sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs)));
+  return tok;
+}
+
+__global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ target, const float* __restrict__ draft,
+                                                     const int64_t* __restrict__ draft_tokens,
+                                                     const float* __restrict__ rand, int32_t* __restrict__ accepted,
+                                                     int64_t* __restrict__ out, int K, int V) {
+  __shared__ float lds[2][kChunk];
+  const int b = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const float* tb = target + static_cast<size_t>(b) * (K + 1) * V;
+  const float* db = draft + static_cast<size_t>(b) * K * V;
+  const int64_t* tok_b = draft_tokens + static_cast<size_t>(b) * K;
+  const float* rb = rand + static_cast<size_t>(b) * K;
+  int64_t* ob = out + static_cast<size_t>(b) * (K + 1);
+
+  // acceptance steps (wave-uniform: every lane reads the same values)
+  int acc = 0;
+  int rej = -1;
+  for (int i = 0; i < K; ++i) {
+    const int64_t t = tok_b[i];
+    const bool in_range = t >= 0 && t < V;
+    const float p = in_range ? tb[static_cast<size_t>(i) * V + t] : 0.0f;
+    const float q = in_range ? db[static_cast<size_t>(i) * V + t] : 0.0f;
+    const float accept_prob = fminf(1.0f, p / (q + 1e-10f));
+    if (rb[i] < accept_prob) {
+      ++acc;
+    } else {
+      rej = i;
+      break;
+    }
+  }
+  if (wave == 0) {
+    if (lane == 0) {
+      // every position is written: accepted tokens, then (after a rejection at
+      // rej) the sample at rej, the bonus at rej + 1 (wave 1) and -1 beyond
+      for (int i = 0; i < acc; ++i) ob[i] = tok_b[i];
+      if (rej >= 0)
+        for (int j = rej + 2; j <= K; ++j) ob[j] = -1;
+      accepted[b] = acc;
+    }
+    if (rej >= 0) {
+      const float* ti = tb + static_cast<size_t>(rej) * V;
+      const float* di = db + static_cast<size_t>(rej) * V;
+      float Z;
+      chain<kZ>(ti, di, V, 0.0f, 0.0f, &Z, lds[0]);
+      const int s = Z > 0.0f ? chain<kResidual>(ti, di, V, Z, rb[rej], nullptr, lds[0])
+                             : chain<kPrefix>(ti, nullptr, V, 0.0f, rb[rej], nullptr, lds[0]);
+      if (lane == 0) ob[rej] = s;
+    }
+  } else {
+    const int row = rej >= 0 ? rej + 1 : K;
+    const float r = rb[rej >= 0 ? min(rej, K - 1) : K - 1];
+    const int bonus = chain<kBonus>(tb + static_cast<size_t>(row) * V, nullptr, V, 0.0f, r, nullptr, lds[1]);
+    if (lane == 0) ob[row] = bonus;
+  }
+}
+
+}  // namespace spec
 }  // namespace fa
 
 using namespace fa;
@@ -172,5 +371,20 @@ extern "C" int fa_token_eviction(const void* k, const void* v, const float* attn
   else
     hipLaunchKernelGGL(compact_kernel<false>, grid, dim3(kThreads), 0, st, kh, vh, keep_mask,
                        static_cast<half_t*>(k_out), static_cast<half_t*>(v_out), H_KV, N, D);
+  return check_launch(fn);
+}
+
+extern "C" int fa_speculative_verify(const float* target_probs, const float* draft_probs, const int64_t* draft_tokens,
+                                     const float* random_vals, int32_t* accepted_count, int64_t* output_tokens, int B,
+                                     int K, int vocab_size, void* stream) {
+  const char* fn = "fa_speculative_verify";
+  if (B < 0 || vocab_size <= 0)
+    return set_error(FA_ERR_INVALID_ARG, "%s: bad sizes (B=%d vocab=%d)", fn, B, vocab_size);
+  if (K < 1 || K > spec::kMaxK) return set_error(FA_ERR_INVALID_ARG, "%s: K=%d outside [1, %d]", fn, K, spec::kMaxK);
+  if (B == 0) return FA_OK;
+  if (!target_probs || !draft_probs || !draft_tokens || !random_vals || !accepted_count || !output_tokens)
+    return set_error(FA_ERR_INVALID_ARG, "%s: null pointer", fn);
+  hipLaunchKernelGGL(spec::verify_kernel, dim3(B), dim3(128), 0, static_cast<hipStream_t>(stream), target_probs,
+                     draft_probs, draft_tokens, random_vals, accepted_count, output_tokens, K, vocab_size);
   return check_launch(fn);
 }

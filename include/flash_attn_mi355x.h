@@ -234,6 +234,25 @@ int fa_token_eviction(const void* k, const void* v, const float* attn_scores,
                       void* k_out, void* v_out, int32_t* keep_mask, int B,
                       int H_KV, int N, int D, int num_evict, void* stream);
 
+/*
+ * Speculative-decoding verification, one batch row per workgroup.
+ *   target_probs fp32 [B, K+1, V], draft_probs fp32 [B, K, V], draft_tokens
+ *   int64 [B, K], random_vals fp32 [B, K]; 1 <= K <= 8.  Writes
+ *   accepted_count int32 [B] and every element of output_tokens int64 [B, K+1]:
+ *   accepted draft tokens; at the first rejection i the residual sample
+ *   (max(target - draft, 0) normalised, or target itself when that is all
+ *   zero), the bonus token from target row i+1 and -1 after it; with no
+ *   rejection the bonus from target row K.  Every running sum is accumulated
+ *   serially in fp32 in vocabulary order, as the reference does; divisions are
+ *   IEEE fp32.  Draft token ids outside [0, V) count as probability 0.
+ * Replaces speculative_verify_forward (flash_attn_kernel.cu:3972-4018), kernel
+ * speculative_verify_kernel (:3853-3970).
+ */
+int fa_speculative_verify(const float* target_probs, const float* draft_probs,
+                          const int64_t* draft_tokens, const float* random_vals,
+                          int32_t* accepted_count, int64_t* output_tokens, int B,
+                          int K, int vocab_size, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -418,3 +418,75 @@ def token_eviction(k, v, attn_scores, num_evict: int):
         k_out[b, :, :kept.numel()] = k[b, :, kept]
         v_out[b, :, :kept.numel()] = v[b, :, kept]
     return k_out, v_out, mask
+
+
+def _first_index_quirk(cond) -> int:
+    """The reference's ``if (cond_v && tok == 0) tok = v`` scan over v ascending
+    (flash_attn_kernel.cu:3914-3918, :3924-3928, :3939-3942, :3960-3964): the first
+    index where cond holds, except that a hit at v = 0 leaves ``tok == 0`` and so
+    is replaced by the next hit; no hit gives 0."""
+    import numpy as np
+
+    hits = np.flatnonzero(cond)
+    if hits.size == 0:
+        return 0
+    if hits[0] != 0:
+        return int(hits[0])
+    return int(hits[1]) if hits.size > 1 else 0
+
+
+def speculative_verify(target_probs, draft_probs, draft_tokens, random_vals, K: int):
+    """``speculative_verify`` (flash_attn_kernel.cu:3853-4018), one batch row at a time.
+
+    fp32 throughout, with every running sum accumulated serially in index
+    order as the reference's single thread does (numpy ``cumsum`` is a serial
+    float32 accumulation): for i < K accept draft token t when
+    ``r_i < fminf(1, p/(q + 1e-10f))`` (:3885-3893); at the first rejection
+    sample from max(target - draft, 0) / Z with r_i (:3900-3919; from target
+    itself when Z == 0, :3920-3930), write -1 after it (:3933-3935) and a bonus
+    token from target row i+1 with r_i (:3937-3945); with no rejection the bonus
+    comes from target row K with r_{K-1} (:3953-3965).  Divisions are IEEE fp32
+    (the reference's fast-math build rounds them approximately; parity at that
+    rounding boundary is unpinned).  Returns (accepted int32 [B], tokens int64 [B, K+1]).
+    """
+    import numpy as np
+
+    tp = target_probs.detach().cpu().numpy().astype(np.float32)
+    dp = draft_probs.detach().cpu().numpy().astype(np.float32)
+    tok = draft_tokens.detach().cpu().numpy().astype(np.int64)
+    rv = random_vals.detach().cpu().numpy().astype(np.float32)
+    B = tp.shape[0]
+    one, eps = np.float32(1.0), np.float32(1e-10)
+    accepted = np.zeros(B, dtype=np.int32)
+    out = np.full((B, K + 1), -1, dtype=np.int64)
+    for b in range(B):
+        acc, rejected = 0, False
+        for i in range(K):
+            t = int(tok[b, i])
+            p_tok, q_tok = tp[b, i, t], dp[b, i, t]
+            accept = min(one, np.float32(p_tok / np.float32(q_tok + eps)))
+            r = rv[b, i]
+            if r < accept:
+                out[b, i] = t
+                acc += 1
+                continue
+            rejected = True
+            diff = (tp[b, i] - dp[b, i]).astype(np.float32)
+            pos = diff > 0
+            Z = np.cumsum(np.where(pos, diff, np.float32(0)), dtype=np.float32)[-1]
+            if Z > 0:
+                terms = np.where(pos, (diff / Z).astype(np.float32), np.float32(0))
+                cs = np.cumsum(terms, dtype=np.float32)
+                out[b, i] = _first_index_quirk(pos & (r < cs))
+            else:
+                cs = np.cumsum(tp[b, i], dtype=np.float32)
+                out[b, i] = _first_index_quirk(r < cs)
+            out[b, i + 1:K] = -1
+            cs = np.cumsum(tp[b, i + 1], dtype=np.float32)
+            out[b, i + 1] = _first_index_quirk(cs >= rv[b, min(i, K - 1)])
+            break
+        if not rejected:
+            cs = np.cumsum(tp[b, K], dtype=np.float32)
+            out[b, K] = _first_index_quirk(cs >= rv[b, K - 1])
+        accepted[b] = acc
+    return torch.from_numpy(accepted), torch.from_numpy(out)

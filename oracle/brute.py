@@ -370,3 +370,73 @@ def token_eviction(k, v, attn_scores, num_evict):
                     v_out[b][h][w] = list(v[b][h][i])
                     w += 1
     return k_out, v_out, masks
+
+
+def speculative_verify(target_probs, draft_probs, draft_tokens, random_vals, K):
+    """speculative_verify_kernel (flash_attn_kernel.cu:3853-3970) as written, on
+    one thread, with numpy float32 scalars for every fp32 operation.  Returns
+    (accepted list, tokens nested list)."""
+    import numpy as np
+
+    f = np.float32
+    tp = np.asarray(target_probs, dtype=np.float32)
+    dp = np.asarray(draft_probs, dtype=np.float32)
+    tok = np.asarray(draft_tokens, dtype=np.int64)
+    rv = np.asarray(random_vals, dtype=np.float32)
+    B, V = tp.shape[0], tp.shape[2]
+    accepted, outs = [], []
+    for b in range(B):
+        out = [-1] * (K + 1)
+        s_acc, s_rej = 0, False
+        for i in range(K):
+            if s_rej:
+                break
+            t = int(tok[b, i])
+            p_tok, q_tok = tp[b, i, t], dp[b, i, t]
+            accept_prob = min(f(1.0), f(p_tok / f(q_tok + f(1e-10))))
+            r = rv[b, i]
+            if r < accept_prob:
+                out[i] = t
+                s_acc += 1
+            else:
+                s_rej = True
+                Z = f(0.0)
+                for v in range(V):
+                    diff = f(tp[b, i, v] - dp[b, i, v])
+                    if diff > f(0.0):
+                        Z = f(Z + diff)
+                if Z > f(0.0):
+                    r2, cumsum, sampled = rv[b, i], f(0.0), 0
+                    for v in range(V):
+                        diff = f(tp[b, i, v] - dp[b, i, v])
+                        if diff > f(0.0):
+                            cumsum = f(cumsum + f(diff / Z))
+                            if r2 < cumsum and sampled == 0:
+                                sampled = v
+                    out[i] = sampled
+                else:
+                    r2, cum, sampled = rv[b, i], f(0.0), 0
+                    for v in range(V):
+                        cum = f(cum + tp[b, i, v])
+                        if r2 < cum and sampled == 0:
+                            sampled = v
+                    out[i] = sampled
+                for j in range(i + 1, K):
+                    out[j] = -1
+                bonus_r, cum, bonus = rv[b, min(i, K - 1)], f(0.0), 0
+                for v in range(V):
+                    cum = f(cum + tp[b, i + 1, v])
+                    if cum >= bonus_r and bonus == 0:
+                        bonus = v
+                out[i + 1] = bonus
+                break
+        if not s_rej:
+            bonus_r, cum, bonus = rv[b, K - 1], f(0.0), 0
+            for v in range(V):
+                cum = f(cum + tp[b, K, v])
+                if cum >= bonus_r and bonus == 0:
+                    bonus = v
+            out[K] = bonus
+        accepted.append(s_acc)
+        outs.append(out)
+    return accepted, outs

@@ -41,3 +41,68 @@ def test_token_eviction_validation(fa):
     big = torch.zeros(1, 1, 1025, 64, dtype=torch.float16, device="cuda")
     with pytest.raises(RuntimeError):
         fa.token_eviction(big, big, torch.zeros(1, 1025, device="cuda"), 1)  # N > 1024
+
+
+# ---------------------------------------------------------------- speculative verify
+
+def _spec(seed, B, K, V, same=False, zero_rand=False):
+    g = torch.Generator().manual_seed(seed)
+    tp = torch.softmax(torch.randn(B, K + 1, V, generator=g), -1)
+    dp = tp[:, :K].clone() if same else torch.softmax(torch.randn(B, K, V, generator=g), -1)
+    tok = torch.randint(0, V, (B, K), generator=g)
+    rv = torch.zeros(B, K) if zero_rand else torch.rand(B, K, generator=g)
+    return tp, dp, tok, rv
+
+
+def _check_spec(fa, tp, dp, tok, rv, K):
+    acc, out = fa.speculative_verify(tp.cuda(), dp.cuda(), tok.cuda(), rv.cuda(), K)
+    racc, rout = A.speculative_verify(tp, dp, tok, rv, K)
+    assert acc.dtype == torch.int32 and out.dtype == torch.int64
+    assert torch.equal(acc.cpu(), racc), (acc.cpu(), racc)
+    assert torch.equal(out.cpu(), rout), (out.cpu(), rout)
+
+
+@pytest.mark.parametrize("seed,B,K,V,same,zero_rand", [
+    (42, 2, 4, 256, False, False),    # test_speculative.py:115-157
+    (42, 4, 5, 128, True, True),      # :160-196 all accepted
+    (7, 2, 3, 32000, False, False),   # :240- large vocabulary
+    (3, 16, 8, 1000, False, False), (4, 3, 1, 257, False, False), (5, 8, 4, 4099, False, False),
+])
+def test_speculative_verify(fa, seed, B, K, V, same, zero_rand):
+    _check_spec(fa, *_spec(seed, B, K, V, same, zero_rand), K)
+
+
+def test_speculative_verify_orthogonal(fa):
+    """test_speculative.py:199-236: disjoint one-hot supports, r = 0.5: rejection at 0."""
+    B, K, V = 2, 4, 64
+    tp = torch.zeros(B, K + 1, V)
+    dp = torch.zeros(B, K, V)
+    for i in range(K + 1):
+        tp[:, i, (i * 10) % V] = 1.0
+    for i in range(K):
+        dp[:, i, (i * 10 + 1) % V] = 1.0
+    _check_spec(fa, tp, dp, torch.full((B, K), 1), torch.full((B, K), 0.5), K)
+
+
+def test_speculative_verify_residual_zero(fa):
+    """Draft dominates target everywhere it differs (Z == 0 path: sample from target)."""
+    B, K, V = 2, 2, 300
+    g = torch.Generator().manual_seed(11)
+    tp = torch.softmax(torch.randn(B, K + 1, V, generator=g), -1)
+    dp = tp[:, :K].clone()
+    tok = torch.randint(0, V, (B, K), generator=g)
+    rv = torch.ones(B, K)  # r = 1 is never < accept_prob <= 1: reject at step 0 with Z == 0
+    _check_spec(fa, tp, dp, tok, rv, K)
+
+
+def test_speculative_verify_validation(fa):
+    tp = torch.rand(1, 3, 10, device="cuda")
+    dp = torch.rand(1, 2, 10, device="cuda")
+    tok = torch.zeros(1, 2, dtype=torch.int64, device="cuda")
+    rv = torch.rand(1, 2, device="cuda")
+    with pytest.raises(RuntimeError):
+        fa.speculative_verify(tp, dp, tok, rv, 3)  # positions mismatch
+    with pytest.raises(RuntimeError):
+        fa.speculative_verify(tp, dp, tok.int(), rv, 2)  # token dtype
+    with pytest.raises(RuntimeError):
+        fa.speculative_verify(torch.rand(1, 10, 10, device="cuda"), dp, tok, rv, 9)  # K > 8

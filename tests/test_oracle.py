@@ -444,3 +444,53 @@ def test_token_eviction_closed_forms():
     assert torch.equal(ko[:, :, :7], k[:, :, :7]) and not ko[:, :, 7:].any()
     ko, vo, m = A.token_eviction(k, v, sc, 0)
     assert torch.equal(ko, k) and torch.equal(vo, v) and bool(m.all())
+
+
+# ---------------------------------------------------------------- speculative verify
+
+def _spec_inputs(seed, B, K, V, mode="random"):
+    g = torch.Generator().manual_seed(seed)
+    tp = torch.softmax(torch.randn(B, K + 1, V, generator=g), -1)
+    if mode == "same":
+        dp = tp[:, :K].clone()
+    else:
+        dp = torch.softmax(torch.randn(B, K, V, generator=g), -1)
+    tok = torch.randint(0, V, (B, K), generator=g)
+    rv = torch.rand(B, K, generator=g)
+    return tp, dp, tok, rv
+
+
+@pytest.mark.parametrize("seed,B,K,V,mode", [(0, 2, 4, 256, "random"), (1, 4, 5, 128, "same"),
+                                             (2, 3, 8, 64, "random"), (3, 2, 1, 100, "random")])
+def test_speculative_verify_vs_brute(seed, B, K, V, mode):
+    tp, dp, tok, rv = _spec_inputs(seed, B, K, V, mode)
+    if mode == "same":
+        rv = torch.zeros(B, K)  # test_speculative.py:152: everything accepted
+    acc, out = A.speculative_verify(tp, dp, tok, rv, K)
+    bacc, bout = Bt.speculative_verify(tp, dp, tok, rv, K)
+    assert acc.tolist() == bacc and out.tolist() == bout
+
+
+def test_speculative_verify_orthogonal_and_quirks():
+    """test_speculative.py:167-200 (one-hot, disjoint supports): rejection at 0;
+    plus the index-0 quirk: a hit at v = 0 is overwritten by the next hit."""
+    B, K, V = 2, 4, 64
+    tp = torch.zeros(B, K + 1, V)
+    dp = torch.zeros(B, K, V)
+    for i in range(K + 1):
+        tp[:, i, (i * 10) % V] = 1.0
+    for i in range(K):
+        dp[:, i, (i * 10 + 1) % V] = 1.0
+    tok = torch.full((B, K), 1)
+    rv = torch.full((B, K), 0.5)
+    acc, out = A.speculative_verify(tp, dp, tok, rv, K)
+    bacc, bout = Bt.speculative_verify(tp, dp, tok, rv, K)
+    assert acc.tolist() == bacc == [0, 0]
+    assert out.tolist() == bout
+    # row 0: residual sampled at v=0 (only hit); bonus from target row 1 (one-hot at 10)
+    assert out[0].tolist() == [0, 10, -1, -1, -1]
+    # quirk: the first hit is v=0 and a later hit exists -> the later one
+    assert A._first_index_quirk([True, False, True, True]) == 2
+    assert A._first_index_quirk([False, True, True]) == 1
+    assert A._first_index_quirk([True]) == 0
+    assert A._first_index_quirk([False, False]) == 0
