@@ -52,6 +52,13 @@ constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many spli
 #define FA_DEC_PAGED_DIV 8
 #endif
 constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / FA_DEC_PAGED_DIV;
+// Every sequence of a fixed-length call (contiguous / INT8 / sliding-window
+// decode) has the same key count, so its splits are all full: about 2.5
+// workgroups per CU balance the per-split merge cost against HBM parallelism.
+#ifndef FA_DEC_TARGET_BLOCKS_FIXED
+#define FA_DEC_TARGET_BLOCKS_FIXED 640
+#endif
+constexpr int kTargetBlocksFixed = FA_DEC_TARGET_BLOCKS_FIXED;
 constexpr int kMaxSplits = 128;
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
@@ -783,9 +790,13 @@ static int check_common(const char* fn, int B, int H_Q, int H_KV, int D) {
 }
 
 template <int MODE>
+static int target_blocks() {
+  return MODE == kModePaged ? kTargetBlocksPaged : (MODE == kModeCB ? kTargetBlocks : kTargetBlocksFixed);
+}
+
+template <int MODE>
 static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, size_t ws_bytes, void* stream) {
-  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D,
-                                  MODE == kModePaged ? kTargetBlocksPaged : kTargetBlocks);
+  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D, target_blocks<MODE>());
   const WorkspaceLayout wl = plan_layout(pl, p.B, p.H_Q, p.H_KV);
   const size_t need = wl.total;
   if (need > 0 && (ws == nullptr || ws_bytes < need))
