@@ -794,6 +794,8 @@ static int target_blocks() {
   return MODE == kModePaged ? kTargetBlocksPaged : (MODE == kModeCB ? kTargetBlocks : kTargetBlocksFixed);
 }
 
+// max_len: keys of the longest sequence the call attends (fixed-length modes:
+// exactly the attended count, which is at most N).
 template <int MODE>
 static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, size_t ws_bytes, void* stream) {
   const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D, target_blocks<MODE>());
@@ -859,7 +861,7 @@ extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void*
   p.o = static_cast<half_t*>(o);
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
   p.fixed_len = causal ? cache_len + 1 : N;
-  return run_decode<kModeDecode>(fn, p, N, workspace, workspace_bytes, stream);
+  return run_decode<kModeDecode>(fn, p, p.fixed_len, workspace, workspace_bytes, stream);
 }
 
 extern "C" int fa_decode_sliding_window_gqa(const void* q, const void* k, const void* v, void* o, int B,
@@ -888,7 +890,7 @@ extern "C" int fa_decode_sliding_window_gqa(const void* q, const void* k, const 
   p.fixed_len = L1 + L2;
   p.seg1 = L1;
   p.seg_shift = static_cast<int>(lo - L1);
-  return run_decode<kModeDecode>(fn, p, N, workspace, workspace_bytes, stream);
+  return run_decode<kModeDecode>(fn, p, p.fixed_len, workspace, workspace_bytes, stream);
 }
 
 extern "C" int fa_continuous_batching_fp16(const void* q, const void* k, const void* v, void* o,
@@ -966,7 +968,7 @@ extern "C" int fa_decode_int8_gqa(const void* q, const void* k, const void* v, v
   p.k_scale = k_scale;
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
   p.fixed_len = cache_len + 1;
-  return run_decode<kModeInt8>(fn, p, N, workspace, workspace_bytes, stream);
+  return run_decode<kModeInt8>(fn, p, p.fixed_len, workspace, workspace_bytes, stream);
 }
 
 extern "C" int fa_decode_int8_kv_cache_gqa(const void* q, const void* k_int8, const void* v_int8,
@@ -989,5 +991,5 @@ extern "C" int fa_decode_int8_kv_cache_gqa(const void* q, const void* k_int8, co
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
   // keys k <= cache_len always (cache_len unchecked: past N every key, below 0 none -> NaN)
   p.fixed_len = static_cast<int>(std::min<long long>(std::max<long long>(static_cast<long long>(cache_len) + 1, 0), N));
-  return run_decode<kModeInt8KV>(fn, p, N, workspace, workspace_bytes, stream);
+  return run_decode<kModeInt8KV>(fn, p, p.fixed_len, workspace, workspace_bytes, stream);
 }
