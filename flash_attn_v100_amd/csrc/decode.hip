@@ -145,19 +145,26 @@ __device__ __forceinline__ u32x2 load_i8x8(const int8_t* row, int col, int d) {
 }
 
 // Eight int8 codes c -> eight fp16 half(c * s), as the reference's
-// __float2half((float)c * scale).  c * s is exact in fp32 (8-bit by 11-bit
-// significands); here it is formed as fma(u, s, -128 s) with u = c + 128 (the
-// code's byte with its top bit flipped, converted by v_cvt_f32_ubyte), whose
-// single rounding of an exactly representable value is exact, then rounded to
-// fp16 to nearest even.
-__device__ __forceinline__ u32x4 dequant_i8x8(u32x2 raw, float s) {
+// __float2half((float)c * scale): c * s is exact in fp32 (8-bit by 11-bit
+// significands), so the result is the exact product rounded once to fp16.
+// Here: flip each code's top bit (u = c + 128), byte-permute u under 0x64 to
+// get the fp16 value 1024 + u, subtract 1152 (exact: c), and multiply by s in
+// packed fp16 -- an IEEE fp16 multiply is that same single rounding of the
+// exact product.  Four permutes, four packed adds, four packed multiplies.
+__device__ __forceinline__ u32x4 dequant_i8x8(u32x2 raw, half_t s) {
   const u32x2 x = raw ^ u32x2{0x80808080u, 0x80808080u};
-  const float nb = -128.0f * s;
-  half8_t h;
+  const half2_t bias = {static_cast<half_t>(-1152.0f), static_cast<half_t>(-1152.0f)};
+  const half2_t sc = {s, s};
+  u32x4 out;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    h[j] = static_cast<half_t>(fmaf(static_cast<float>((x[j >> 2] >> (8 * (j & 3))) & 0xFFu), s, nb));
-  return __builtin_bit_cast(u32x4, h);
+  for (int w = 0; w < 2; ++w) {
+    // perm(hi, lo, sel): selector byte k picks byte k' of lo (0-3) or of hi (4-7)
+    const uint32_t lo2 = __builtin_amdgcn_perm(0x64646464u, x[w], 0x05010400u);  // u0, u1 -> 1024 + u
+    const uint32_t hi2 = __builtin_amdgcn_perm(0x64646464u, x[w], 0x05030402u);  // u2, u3
+    out[2 * w] = as_u32((as_h2(lo2) + bias) * sc);
+    out[2 * w + 1] = as_u32((as_h2(hi2) + bias) * sc);
+  }
+  return out;
 }
 
 // Per-wave LDS scratch used to hand probabilities from the MFMA layout (lane =
@@ -336,8 +343,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   struct Tile8 {
     u32x2 k[T16][NC];
     u32x2 v[UV];
-    float ks[T16];
-    float vs[UV];
+    half_t ks[T16];
+    half_t vs[UV];
   };
   auto load_tile8 = [&](Tile8& T, int t0) {
     const int8_t* kh = p.k8 + kv_head_base;
@@ -346,14 +353,14 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 #pragma unroll
     for (int tt = 0; tt < T16; ++tt) {
       const int t = min(t0 + 16 * tt + l16, klast);
-      T.ks[tt] = static_cast<float>(p.k_sc[sbase + t]);
+      T.ks[tt] = p.k_sc[sbase + t];
 #pragma unroll
       for (int c = 0; c < NC; ++c) T.k[tt][c] = load_i8x8<VEC>(kh + static_cast<size_t>(t) * D, 32 * c + 8 * q4, D);
     }
 #pragma unroll
     for (int u = 0; u < UV; ++u) {
       const int t = min(t0 + u * RPW + rg, klast);
-      T.vs[u] = static_cast<float>(p.v_sc[sbase + t]);
+      T.vs[u] = p.v_sc[sbase + t];
       T.v[u] = load_i8x8<VEC>(vh + static_cast<size_t>(t) * D, col, D);
     }
   };
