@@ -747,7 +747,10 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
   const dim3 grid(train_grid(p));
   hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
   // fp16 at D > 64 splits dV and dK into two passes to fit 256 VGPRs
-  if constexpr (sizeof(T) == 2 && DP > 64) {
+#ifndef FA_BWD_SPLIT_DKDV
+#define FA_BWD_SPLIT_DKDV 1
+#endif
+  if constexpr (FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64) {
     hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, st, p);
     hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);
   } else {
