@@ -85,6 +85,7 @@ struct DecodeParams {
   int chunk, num_splits, num_hg;
   int max_num_blocks, num_pages;
   int lpt;                     // CB / paged: serve sequences longest first
+  int absorb_tail;             // fixed-length: the last split runs to fixed_len
   int seg1, seg_shift;         // contiguous modes: key v < seg1 is row v, later keys row v + seg_shift
                                // (seg_shift = 0: identity; sliding window: sink run, then window run)
   float scale_log2;            // (1/sqrt(D)) * log2(e)
@@ -234,7 +235,9 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 
   const int L = seq_len_of<MODE>(p, b);
   const int k0 = split * p.chunk;
-  const int k1 = min(L, k0 + p.chunk);
+  // With absorb_tail (fixed-length calls only) the last split also takes the
+  // short remainder past (S - 1) * chunk; it stays within kMaxChunk keys.
+  const int k1 = (p.absorb_tail && split == S - 1) ? L : min(L, k0 + p.chunk);
 
   if (k0 >= k1) {
     // No key at all (L <= 0): the reference's acc/l_i is 0/0 there.  Split 0
@@ -713,7 +716,12 @@ static int pick_dp(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
 // Query heads per workgroup: one 16-row MFMA tile holds up to 16 heads of a group.
 static int pick_gb(int g) { return g <= 1 ? 1 : (g <= 2 ? 2 : (g <= 4 ? 4 : (g <= 8 ? 8 : 16))); }
 
-static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int target_blocks) {
+// absorb_tail (fixed-length calls): when the keys past the last full chunk
+// are at most a quarter chunk, the last full split takes them too instead of
+// a split of its own (e.g. 4097 keys in 256-key splits: 16 splits, not 17 --
+// one workgroup and one merge round trip less).
+static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int target_blocks,
+                            bool absorb_tail = false) {
   DecodePlan pl;
   const int G = H_Q / H_KV;
   pl.dp = pick_dp(D);
@@ -729,6 +737,10 @@ static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int ta
   if (chunk > kMaxChunk) chunk = kMaxChunk;
   pl.chunk = static_cast<int>(chunk);
   pl.splits = max_len > 0 ? ceil_div(max_len, chunk) : 1;
+  if (absorb_tail && pl.splits > 1) {
+    const long long tail = max_len - (pl.splits - 1) * chunk;
+    if (tail <= chunk / 4 && chunk + tail <= kMaxChunk) --pl.splits;
+  }
   return pl;
 }
 
@@ -805,7 +817,9 @@ static int target_blocks() {
 // exactly the attended count, which is at most N).
 template <int MODE>
 static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, size_t ws_bytes, void* stream) {
-  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D, target_blocks<MODE>());
+  constexpr bool kFixed = MODE == kModeDecode || MODE == kModeInt8 || MODE == kModeInt8KV;
+  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D, target_blocks<MODE>(), kFixed);
+  p.absorb_tail = kFixed ? 1 : 0;
   const WorkspaceLayout wl = plan_layout(pl, p.B, p.H_Q, p.H_KV);
   const size_t need = wl.total;
   if (need > 0 && (ws == nullptr || ws_bytes < need))
