@@ -225,7 +225,9 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
 
   // key ranges: the workgroup walks to its last wave's diagonal, each wave stops at its own
   const int kend_wg = p.causal ? min(seq_len, q0 + BQ) : seq_len;
-  const int kend_w = p.causal ? min(seq_len, wq0 + RW) : seq_len;
+  // a wave whose rows all lie past the written rows computes nothing (it still
+  // copies its share of every tile and joins the barriers)
+  const int kend_w = wq0 >= rows ? 0 : (p.causal ? min(seq_len, wq0 + RW) : seq_len);
   const int ntiles = (kend_wg + kBK - 1) / kBK;
 
   // ---- tile copies: slot g = (wave*IPW + i)*64 + lane of a tile holds logical

@@ -505,7 +505,8 @@ __global__ __launch_bounds__(kThreads) void query_major_kernel(TrainParams p) {
   const float c = p.scale_log2;
 
   const int kend = p.causal ? min(N, q0 + kBlockRows) : N;  // keys this workgroup needs
-  const int kend_w = p.causal ? min(N, wq0 + kRows) : N;     // keys this wave needs
+  // keys this wave needs (none when all its rows lie past N)
+  const int kend_w = wq0 >= N ? 0 : (p.causal ? min(N, wq0 + kRows) : N);
   const int ntiles = (kend + kRows - 1) / kRows;
 
   Ring ring(smem, tid, D);
@@ -652,7 +653,7 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(TrainParams p) {
   const Reader<T, DP> rd(lane);
   // a tile whose last query precedes this wave's first key contributes nothing:
   // causal waves start at the tile holding query wk0
-  const int c_begin = p.causal ? (wk0 - qstart) / kRows : 0;
+  const int c_begin = wk0 >= N ? ntiles : (p.causal ? (wk0 - qstart) / kRows : 0);  // no keys: no compute
   run_ring<Ring, DMA, VEC>(ring, qp, dop, lse, dlt, qstart, ntiles, c_begin, ntiles, N, D, [&](int stage, int t) {
     const int qt = qstart + t * kRows;
     const unsigned qs = ring.addr_a(stage);
