@@ -666,3 +666,19 @@ def test_sliding_window_reference_case(fa):
     q, k, v = randn(g, 2, 8, 1, 64), randn(g, 2, 2, 256, 64), randn(g, 2, 2, 256, 64)
     out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, 255, 64, 4)
     assert_close(out, A.decode_sliding_window(q, k, v, 255, 64, 4), what="sliding reference case")
+
+
+@pytest.mark.parametrize("n", [1025, 1087, 1088, 1089, 2049, 4097, 4160, 4161])
+def test_decode_split_tail_boundaries(fa, n):
+    """Fixed-length decode folds a key remainder of at most a quarter chunk into
+    the last split (256-key chunks here: remainders 1, 63, 64 folded; 65 not)."""
+    g = gen(n)
+    q, k, v = randn(g, 1, 32, 1, 128), randn(g, 1, 8, n, 128), randn(g, 1, 8, n, 128)
+    out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, n - 1)
+    assert_close(out, A.decode(q, k, v, True, n - 1), what=f"decode tail n={n}")
+    # the same sequence length through the INT8 path (same split plan)
+    qs = (q.float().abs().amax(-1).squeeze(-1) / 127).contiguous()
+    ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(1, 8, n).contiguous()
+    o8 = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), n - 1)
+    r8 = A.decode_int8(q, k, v, qs, ks, n - 1)
+    assert rel_l2(o8, r8) <= INT8_REL_L2
