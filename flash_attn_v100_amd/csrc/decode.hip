@@ -496,21 +496,33 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
 
-    // -- O += P V in the row layout
+    // -- O += P V in the row layout, two keys (loads u and u + 1: keys kl and
+    //    kl + RPW) per v_dot2_f32_f16: P rounded to fp16 (as in the prefill's
+    //    P V product), products exact, fp32 accumulation.
+    static_assert(UV % 2 == 0, "V loads pair up");
 #pragma unroll
-    for (int u = 0; u < UV; ++u) {
-      const int kl = u * RPW + rg;  // key index inside this iteration's tile
-      float pv[GP];
+    for (int u = 0; u < UV; u += 2) {
+      const int kl = u * RPW + rg;  // key of load u inside this iteration's tile
+      half2_t pp[GP];
 #pragma unroll
       for (int g4 = 0; g4 < GP; g4 += 4) {
-        const float4_t x = *reinterpret_cast<const float4_t*>(&s_p[wave][kl][g4]);
-        pv[g4] = x[0]; pv[g4 + 1] = x[1]; pv[g4 + 2] = x[2]; pv[g4 + 3] = x[3];
+        const float4_t x0 = *reinterpret_cast<const float4_t*>(&s_p[wave][kl][g4]);
+        const float4_t x1 = *reinterpret_cast<const float4_t*>(&s_p[wave][kl + RPW][g4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pp[g4 + e] = half2_t{static_cast<half_t>(x0[e]), static_cast<half_t>(x1[e])};
       }
-      const half8_t vh = __builtin_bit_cast(half8_t, T.v[u]);
 #pragma unroll
-      for (int g = 0; g < GB; ++g)
+      for (int w = 0; w < 4; ++w) {
+        // columns 2w, 2w+1 of both keys: {v_u[2w], v_u+1[2w]} and {v_u[2w+1], v_u+1[2w+1]}
+        const uint32_t a = T.v[u][w], b = T.v[u + 1][w];
+        const half2_t ve = as_h2(__builtin_amdgcn_perm(b, a, 0x05040100u));
+        const half2_t vo = as_h2(__builtin_amdgcn_perm(b, a, 0x07060302u));
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(pv[g], static_cast<float>(vh[j]), acc[g][j]);
+        for (int g = 0; g < GB; ++g) {
+          acc[g][2 * w] = __builtin_amdgcn_fdot2(pp[g], ve, acc[g][2 * w], false);
+          acc[g][2 * w + 1] = __builtin_amdgcn_fdot2(pp[g], vo, acc[g][2 * w + 1], false);
+        }
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
