@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     }
   }
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   // MFMA layout: lane = (key l16 of a 16-key tile, quarter q)
   const int l16 = lane & 15;
   const int q4 = lane >> 4;
