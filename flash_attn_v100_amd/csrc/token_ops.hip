@@ -290,7 +290,7 @@ __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ t
                                                      const int64_t* __restrict__ draft_tokens,
                                                      const float* __restrict__ rand, int32_t* __restrict__ accepted,
                                                      int64_t* __restrict__ out, int K, int V) {
-  __shared__ float lds[2][kChunk];
+  __shared__ __attribute__((aligned(16))) float lds[2][kChunk];  // per-wave term / running-sum staging
   const int b = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
