@@ -88,15 +88,19 @@ struct PrefillParams {
 #ifndef FA_PRE_W128
 #define FA_PRE_W128 3
 #endif
-template <int DP>
+// WIDE (D <= 64 only): 64-key tiles for launches of at most about one
+// residency round of workgroups, where fewer, longer tiles per barrier win
+// (measured 5-12 % on N <= 1024); larger launches keep 32-key tiles.
+template <int DP, bool WIDE = false>
 struct PrefillShape {
   static constexpr int RB = DP <= 64 ? FA_PRE_RB64 : 1;                 // 32-row query blocks per wave
   static constexpr int RW = 32 * RB;                                    // query rows per wave
   static constexpr int BQ = kPreWaves * RW;                             // query rows per workgroup
-  static constexpr int BK = DP <= 64 ? FA_PRE_BK64 : 32;                // keys per tile
+  static constexpr int BK = DP <= 64 ? (WIDE ? 64 : FA_PRE_BK64) : 32;  // keys per tile
   static constexpr int NS = DP <= 64 ? 3 : (DP <= 128 ? FA_PRE_NS128 : 2);  // LDS ring stages
   static constexpr int TILE = BK * DP;                                  // halves per K (or V) tile
-  static constexpr int WAVES_PER_SIMD = DP <= 64 ? FA_PRE_W64 : (DP <= 128 ? FA_PRE_W128 : 2);  // register budget target
+  static constexpr int WAVES_PER_SIMD =
+      DP <= 64 ? (WIDE ? 3 : FA_PRE_W64) : (DP <= 128 ? FA_PRE_W128 : 2);  // register budget target
 };
 
 // Varlen output rows that no sequence's attention writes are set to zero by
@@ -132,10 +136,10 @@ __device__ void zero_unwritten_rows(const PrefillParams& p, int z) {
   }
 }
 
-template <int DP, bool VARLEN, bool VEC>
+template <int DP, bool VARLEN, bool VEC, bool WIDE = false>
 __global__ __launch_bounds__(kPreThreads)
-__attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void prefill_kernel(PrefillParams p) {
-  using Shape = PrefillShape<DP>;
+__attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) void prefill_kernel(PrefillParams p) {
+  using Shape = PrefillShape<DP, WIDE>;
   constexpr int RB = Shape::RB;
   constexpr int RW = Shape::RW;
   constexpr int BQ = Shape::BQ;
@@ -150,7 +154,7 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
   constexpr float kRescaleLimit = 256.0f;  // 2^8: largest p before the max is refreshed
   static_assert(IPW * 8 * 64 * kPreWaves == TILE, "tile must split evenly over the waves");
 
-  __shared__ __attribute__((aligned(1024))) half_t smem[NS * 2 * PrefillShape<DP>::TILE];
+  __shared__ __attribute__((aligned(1024))) half_t smem[NS * 2 * Shape::TILE];
 
   const int D = p.D;
   if constexpr (VARLEN) {
@@ -453,13 +457,14 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP>::WAVES_PER_SIMD))) void pref
   }
 }
 
-template <int DP, bool VARLEN>
+template <int DP, bool VARLEN, bool WIDE = false>
 static void launch_prefill(bool vec, int blocks, const PrefillParams& p, hipStream_t st) {
   if (vec)
-    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, true>), dim3(blocks), dim3(kPreThreads), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, true, WIDE>), dim3(blocks), dim3(kPreThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, false>), dim3(blocks), dim3(kPreThreads), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, false, WIDE>), dim3(blocks), dim3(kPreThreads), 0, st, p);
 }
+constexpr long long kWideMaxBlocks = 1024;  // D <= 64 launches up to this size use 64-key tiles
 
 static int prefill_bq(int D) { return D <= 64 ? PrefillShape<64>::BQ : (D <= 128 ? PrefillShape<128>::BQ : PrefillShape<256>::BQ); }
 
@@ -482,7 +487,10 @@ static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, Prefi
   if (blocks > 0x7fffffffLL) return set_error(FA_ERR_UNSUPPORTED, "%s: problem too large for one launch", fn);
   if (blocks == 0) return FA_OK;
   p.zero_base = static_cast<int>(main_blocks);
-  if (D <= 64) launch_prefill<64, VARLEN>(vec, static_cast<int>(blocks), p, st);
+  if (D <= 64) {
+    if (main_blocks <= kWideMaxBlocks) launch_prefill<64, VARLEN, true>(vec, static_cast<int>(blocks), p, st);
+    else launch_prefill<64, VARLEN>(vec, static_cast<int>(blocks), p, st);
+  }
   else if (D <= 128) launch_prefill<128, VARLEN>(vec, static_cast<int>(blocks), p, st);
   else launch_prefill<256, VARLEN>(vec, static_cast<int>(blocks), p, st);
   return check_launch(fn);
