@@ -8,7 +8,9 @@ cases).  The reference ships no golden vectors, so these fixtures freeze the
 independent restatement; tests/test_oracle.py checks the vectorised oracle
 against them and the GPU tests check the kernels against the oracle.
 
-Run:  python tests/golden/make_golden.py
+Run:  python tests/golden/make_golden.py               (every fixture)
+      python tests/golden/make_golden.py --next-rows   (only the LSE forward, backward,
+      sliding-window, INT8-KV-cache, token-eviction and speculative-verify fixtures)
 """
 import os
 import sys
@@ -27,6 +29,12 @@ def rn(g, *s):
 
 def save(name, kind, args, out):
     torch.save({"kind": kind, "args": args, "out": torch.tensor(out, dtype=torch.float64)},
+               os.path.join(HERE, name + ".pt"))
+    print("wrote", name)
+
+
+def save_multi(name, kind, args, outs, dtype=torch.float64):
+    torch.save({"kind": kind, "args": args, "outs": [torch.tensor(o, dtype=dtype) for o in outs]},
                os.path.join(HERE, name + ".pt"))
     print("wrote", name)
 
@@ -92,5 +100,56 @@ def main():
          Bt.decode_int8(q, k.float(), v.double(), qs, ks, 6))
 
 
+def next_rows():
+    """Fixtures for the entry points beyond the eight hot-path ones."""
+    # LSE forward and backward: the reference test_backward.py shape family (D=32 there; 8 here)
+    g = torch.Generator().manual_seed(7)
+    q, k, v, do = (torch.randn(1, 2, 9, 8, generator=g, dtype=torch.float64) for _ in range(4))
+    out, lse = Bt.prefill_lse(q, k, v, True)
+    save_multi("prefill_lse_causal", "prefill_lse", dict(q=q, k=k, v=v, causal=True), [out, lse])
+    ot, lt = torch.tensor(out, dtype=torch.float64), torch.tensor(lse, dtype=torch.float64)
+    save_multi("backward_causal", "backward", dict(dout=do, q=q, k=k, v=v, out=ot, lse=lt, causal=True),
+               list(Bt.backward(do, q, k, v, ot, lt, True)))
+
+    # sliding window + sink, INT8 KV cache
+    g = torch.Generator().manual_seed(11)
+    q, k, v = rn(g, 1, 4, 1, 8), rn(g, 1, 2, 30, 8), rn(g, 1, 2, 30, 8)
+    save_multi("sliding_window", "sliding_window", dict(q=q, k=k, v=v, cache_len=25, window=7, sink=3),
+               [Bt.decode_sliding_window(q.double(), k.double(), v.double(), 25, 7, 3)])
+    g = torch.Generator().manual_seed(12)
+    q = rn(g, 1, 4, 1, 8)
+    k8 = torch.randint(-128, 128, (1, 2, 12, 8), generator=g, dtype=torch.int8)
+    v8 = torch.randint(-128, 128, (1, 2, 12, 8), generator=g, dtype=torch.int8)
+    ksc = (torch.rand(1, 2, 12, generator=g) * 0.02 + 0.001).half()
+    vsc = (torch.rand(1, 2, 12, generator=g) * 0.02 + 0.001).half()
+    save_multi("int8_kv_cache", "int8_kv_cache", dict(q=q, k_i8=k8, v_i8=v8, k_scale=ksc, v_scale=vsc, cache_len=9),
+               [Bt.decode_int8_kv_cache(q, k8, v8, ksc, vsc, 9)])
+
+    # token eviction with ties
+    g = torch.Generator().manual_seed(13)
+    k, v = rn(g, 2, 2, 10, 4), rn(g, 2, 2, 10, 4)
+    sc = torch.randint(0, 4, (2, 10), generator=g).float()
+    ko, vo, m = Bt.token_eviction(k, v, sc, 4)
+    torch.save({"kind": "token_eviction", "args": dict(k=k, v=v, attn_scores=sc, num_evict=4),
+                "outs": [torch.tensor(ko, dtype=torch.float16), torch.tensor(vo, dtype=torch.float16),
+                         torch.tensor(m, dtype=torch.int32)]}, os.path.join(HERE, "token_eviction.pt"))
+    print("wrote token_eviction")
+
+    # speculative verify (test_speculative.py:115-157 shape family, smaller vocabulary)
+    g = torch.Generator().manual_seed(42)
+    tp = torch.softmax(torch.randn(2, 5, 64, generator=g), -1)
+    dp = torch.softmax(torch.randn(2, 4, 64, generator=g), -1)
+    tok = torch.randint(0, 64, (2, 4), generator=g)
+    rv = torch.rand(2, 4, generator=g)
+    acc, outs = Bt.speculative_verify(tp, dp, tok, rv, 4)
+    torch.save({"kind": "speculative_verify", "args": dict(target_probs=tp, draft_probs=dp, draft_tokens=tok,
+                                                           random_vals=rv, K=4),
+                "outs": [torch.tensor(acc, dtype=torch.int32), torch.tensor(outs, dtype=torch.int64)]},
+               os.path.join(HERE, "speculative_verify.pt"))
+    print("wrote speculative_verify")
+
+
 if __name__ == "__main__":
-    main()
+    if "--next-rows" not in sys.argv[1:]:
+        main()
+    next_rows()

@@ -253,7 +253,7 @@ def _golden_files():
 
 
 def test_golden_fixtures_present():
-    assert len(_golden_files()) >= 6
+    assert len(_golden_files()) >= 13
 
 
 @pytest.mark.parametrize("fname", _golden_files())
@@ -275,6 +275,35 @@ def test_oracle_matches_golden(fname):
                                bool(a["causal"]), F64)
     elif kind == "int8":
         out = A.decode_int8(a["q"], a["k"], a["v"], a["q_scale"], a["k_scale"], int(a["cache_len"]), F64)
+    elif kind == "prefill_lse":
+        for got, exp in zip(A.prefill_lse(a["q"], a["k"], a["v"], bool(a["causal"]), F64), fx["outs"]):
+            close(got, exp, tol=1e-9)
+        return
+    elif kind == "backward":
+        got = A.backward(a["dout"], a["q"], a["k"], a["v"], a["out"], a["lse"], bool(a["causal"]))
+        for g_, exp in zip(got, fx["outs"]):
+            close(g_, exp, tol=1e-9)
+        return
+    elif kind == "sliding_window":
+        out = A.decode_sliding_window(a["q"], a["k"], a["v"], int(a["cache_len"]), int(a["window"]),
+                                      int(a["sink"]), F64)
+        close(out, fx["outs"][0], tol=1e-6)
+        return
+    elif kind == "int8_kv_cache":
+        out = A.decode_int8_kv_cache(a["q"], a["k_i8"], a["v_i8"], a["k_scale"], a["v_scale"],
+                                     int(a["cache_len"]), F64)
+        close(out, fx["outs"][0], tol=1e-6)
+        return
+    elif kind == "token_eviction":
+        got = A.token_eviction(a["k"], a["v"], a["attn_scores"], int(a["num_evict"]))
+        for g_, exp in zip(got, fx["outs"]):
+            assert torch.equal(g_, exp)
+        return
+    elif kind == "speculative_verify":
+        acc, toks = A.speculative_verify(a["target_probs"], a["draft_probs"], a["draft_tokens"],
+                                         a["random_vals"], int(a["K"]))
+        assert torch.equal(acc, fx["outs"][0]) and torch.equal(toks, fx["outs"][1])
+        return
     else:
         raise AssertionError(kind)
     close(out, fx["out"], tol=1e-6)
