@@ -129,3 +129,32 @@ def test_training_validation_errors(fa):
         fa.backward(q32, q32, q32, q32, out, lse.double(), True)  # lse dtype
     with pytest.raises(RuntimeError):
         fa.backward(q32.half(), q32, q32, q32, out, lse, True)  # dout dtype
+
+
+def test_backward_bench_shape_sampled(fa):
+    """Config 7's full shape (B=4 H=16 N=2048 D=128 causal, fp16): every gradient
+    computed on the GPU, three (batch, head) slices checked against the oracle."""
+    g = gen(70)
+    B, H, N, D = 4, 16, 2048, 128
+    q, k, v, do = (randn(g, B, H, N, D) for _ in range(4))
+    qc, kc, vc, dc = cuda(q, k, v, do)
+    out, lse = fa.forward_fp16_with_lse(qc, kc, vc, True)
+    dq, dk, dv = fa.backward(dc, qc, kc, vc, out, lse, True)
+    oc, lc = out.cpu(), lse.cpu()
+    for b, h in ((0, 0), (2, 7), (3, 15)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ref = A.backward(do[sl], q[sl], k[sl], v[sl], oc[sl], lc[sl], True)
+        _check_grads((dq.cpu()[sl], dk.cpu()[sl], dv.cpu()[sl]), ref, True, f"bench shape b={b} h={h}")
+
+
+def test_forward_fp32_bench_shape_sampled(fa):
+    """Config 7b's forward (fp32, B=4 H=16 N=2048 D=128 causal) on sampled slices."""
+    g = gen(71)
+    B, H, N, D = 4, 16, 2048, 128
+    q, k, v = (randn(g, B, H, N, D, dtype=torch.float32) for _ in range(3))
+    out, lse = fa.forward_with_lse(*cuda(q, k, v), True)
+    for b, h in ((1, 3), (3, 12)):
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ro, rl = A.prefill_lse(q[sl], k[sl], v[sl], True, compute_dtype=F64)
+        assert_close(out.cpu()[sl], ro, atol=2e-4, rtol=2e-4, what="fp32 forward bench shape")
+        assert_close(lse.cpu()[sl], rl, atol=2e-4, rtol=2e-4, what="fp32 lse bench shape")
