@@ -95,6 +95,23 @@ def test_speculative_verify_residual_zero(fa):
     _check_spec(fa, tp, dp, tok, rv, K)
 
 
+def test_speculative_verify_zero_hit_across_chunks(fa):
+    """A residual hit at index 0 defers to the next contributing index, 1500
+    elements (more than one 1024-element scan chunk) later."""
+    V = 3000
+    g = torch.Generator().manual_seed(12)
+    tp = torch.zeros(1, 2, V)
+    tp[0, 0, 0] = tp[0, 0, 1500] = 0.5
+    tp[0, 1] = torch.softmax(torch.randn(V, generator=g), -1)
+    dp = torch.full((1, 1, V), 1.0 / (V - 2))
+    dp[0, 0, 0] = dp[0, 0, 1500] = 0.0
+    tok = torch.tensor([[7]])  # target mass 0: rejected at step 0
+    rv = torch.tensor([[0.3]])
+    _check_spec(fa, tp, dp, tok, rv, 1)
+    _, rout = A.speculative_verify(tp, dp, tok, rv, 1)
+    assert int(rout[0, 0]) == 1500
+
+
 def test_speculative_verify_validation(fa):
     tp = torch.rand(1, 3, 10, device="cuda")
     dp = torch.rand(1, 2, 10, device="cuda")
