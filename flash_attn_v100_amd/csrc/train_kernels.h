@@ -341,6 +341,14 @@ struct TileRing {
   }
 };
 
+// The fp16 key-major passes walk their query tiles last to first (0: first
+// to last): the 128-key blocks of one (batch, head) run together on one XCD
+// and all end at the last query tile, so walking backwards they read each Q /
+// dO tile at about the same time and share it through L2.
+#ifndef FA_BWD_REV
+#define FA_BWD_REV 1
+#endif
+
 struct TrainParams {
   const void* q;
   const void* k;
@@ -390,35 +398,46 @@ inline int train_grid(const TrainParams& p) {
 // copies and joins the barriers of all tiles).  The three tile ranges are
 // separate loops so that the accumulating loop carries no per-tile branch
 // around the MFMAs (which would make the compiler copy the accumulators).
-template <typename Ring, bool DMA, bool VEC, typename T, typename Compute>
+// REV walks the tiles last to first (`tile` passed to compute is still the
+// tile's index from r_first): workgroups that share a stream but start at
+// different tiles and end together then read each tile at about the same
+// time, so the copies after the first hit L2.
+template <typename Ring, bool DMA, bool VEC, bool REV = false, typename T, typename Compute>
 __device__ __forceinline__ void run_ring(Ring& ring, const T* pa, const T* pb, const float* va, const float* vb,
                                          int r_first, int ntiles, int c_begin, int c_end, int rows, int d,
                                          Compute&& compute) {
   c_begin = max(0, min(c_begin, ntiles));
   c_end = max(c_begin, min(c_end, ntiles));
+  if constexpr (REV) {
+    const int b = ntiles - c_end;
+    c_end = ntiles - c_begin;
+    c_begin = b;
+  }
+  auto tile_of = [&](int t) { return REV ? ntiles - 1 - t : t; };  // stream position -> tile
+  auto row_of = [&](int t) { return r_first + tile_of(t) * kRows; };
   if constexpr (DMA) {
     constexpr int NS = Ring::NS;
 #pragma unroll
     for (int s = 0; s < NS - 1; ++s)
-      if (s < ntiles) ring.dma(pa, pb, va, vb, r_first + s * kRows, rows, d, s);
+      if (s < ntiles) ring.dma(pa, pb, va, vb, row_of(s), rows, d, s);
     auto step = [&](int t) {
       ring.wait_dma(t + 1 < ntiles);  // this wave's copies of tile t landed
       tile_barrier();                  // everyone's did; stage (t - 1) % NS is free
-      if (t + NS - 1 < ntiles) ring.dma(pa, pb, va, vb, r_first + (t + NS - 1) * kRows, rows, d, (t + NS - 1) % NS);
+      if (t + NS - 1 < ntiles) ring.dma(pa, pb, va, vb, row_of(t + NS - 1), rows, d, (t + NS - 1) % NS);
     };
     for (int t = 0; t < c_begin; ++t) step(t);
     for (int t = c_begin; t < c_end; ++t) {
       step(t);
-      compute(t % NS, t);
+      compute(t % NS, tile_of(t));
     }
     for (int t = c_end; t < ntiles; ++t) step(t);
   } else {
     if (ntiles > 0) {
-      ring.template load<VEC>(pa, pb, va, vb, r_first, rows, d);
+      ring.template load<VEC>(pa, pb, va, vb, row_of(0), rows, d);
       ring.store(0);
     }
     auto pre = [&](int t) {
-      if (t + 1 < ntiles) ring.template load<VEC>(pa, pb, va, vb, r_first + (t + 1) * kRows, rows, d);
+      if (t + 1 < ntiles) ring.template load<VEC>(pa, pb, va, vb, row_of(t + 1), rows, d);
       __syncthreads();
     };
     auto post = [&](int t) {
@@ -430,7 +449,7 @@ __device__ __forceinline__ void run_ring(Ring& ring, const T* pa, const T* pb, c
     }
     for (int t = c_begin; t < c_end; ++t) {
       pre(t);
-      compute(t & 1, t);
+      compute(t & 1, tile_of(t));
       post(t);
     }
     for (int t = c_end; t < ntiles; ++t) {
@@ -654,7 +673,8 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(TrainParams p) {
   // a tile whose last query precedes this wave's first key contributes nothing:
   // causal waves start at the tile holding query wk0
   const int c_begin = wk0 >= N ? ntiles : (p.causal ? (wk0 - qstart) / kRows : 0);  // no keys: no compute
-  run_ring<Ring, DMA, VEC>(ring, qp, dop, lse, dlt, qstart, ntiles, c_begin, ntiles, N, D, [&](int stage, int t) {
+  // (the register-staged fp32 pass measured no gain from it)
+  run_ring<Ring, DMA, VEC, FA_BWD_REV != 0 && DMA>(ring, qp, dop, lse, dlt, qstart, ntiles, c_begin, ntiles, N, D, [&](int stage, int t) {
     const int qt = qstart + t * kRows;
     const unsigned qs = ring.addr_a(stage);
     const unsigned ds = ring.addr_b(stage);
