@@ -89,7 +89,9 @@ def test_backward_reference_case(fa, dtype, causal):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("b,h,n,d", SHAPES[1:] + [(1, 2, 512, 128), (2, 2, 257, 64)])
+# (3, 4, 333, 128) and (2, 5, 150, 64): at least 8 (batch, head) units (the
+# XCD-grouped block order) with a partial last tile
+@pytest.mark.parametrize("b,h,n,d", SHAPES[1:] + [(1, 2, 512, 128), (2, 2, 257, 64), (3, 4, 333, 128), (2, 5, 150, 64)])
 def test_backward_shapes(fa, dtype, causal, b, h, n, d):
     g = gen(300 + n * 3 + d)
     q, k, v, do = (randn(g, b, h, n, d, dtype=dtype) for _ in range(4))
