@@ -2,11 +2,31 @@
 // attention backward, and the instantiations of the fp16 backward and fp32
 // forward kernels (built with MFMA accumulators in VGPRs; the fp32 backward
 // lives in train_fp32.hip).
+#include <mutex>
+
 #include "capi_internal.h"
 #include "train_kernels.h"
 
 namespace fa {
 namespace train {
+
+hipStream_t backward_side_stream() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static hipStream_t streams[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (streams[dev] == nullptr) {
+    hipStream_t s = nullptr;
+    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+      (void)hipGetLastError();  // leave no sticky error for check_launch
+      return nullptr;
+    }
+    streams[dev] = s;
+  }
+  return streams[dev];
+}
 
 static int check_sizes(const char* fn, int B, int H, int N, int D) {
   if (B < 0 || H <= 0 || N < 0 || D <= 0)

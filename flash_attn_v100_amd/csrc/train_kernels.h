@@ -763,14 +763,46 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(TrainParams p) {
 // Launch helpers (the backward is instantiated per element type by train.hip
 // and train_fp32.hip; the fp32 forward, which fits 256 VGPRs, by train.hip).
 
+// A non-blocking, default-priority stream of the current device for the
+// backward's concurrent dV pass (created on first use, kept for the process;
+// nullptr if it cannot be created).  Defined in train.hip.
+hipStream_t backward_side_stream();
+
 template <typename T, int DP, bool VEC>
 void launch_backward_dp(const TrainParams& p, hipStream_t st) {
   const dim3 grid(train_grid(p));
-  hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
   // fp16 at D > 64 splits dV and dK into two passes to fit 256 VGPRs
 #ifndef FA_BWD_SPLIT_DKDV
 #define FA_BWD_SPLIT_DKDV 1
 #endif
+  if constexpr (FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64) {
+    // The dV pass needs neither delta nor dQ: it runs on a side stream,
+    // forked from and joined back into `st`, concurrently with the dQ kernel
+    // and the dK pass (each of them leaves most of the MFMA pipe idle).
+    // (not while `st` is being captured into a graph: the capture then keeps
+    // the three launches in order on `st`)
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(st, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
+    hipStream_t side = capturing ? nullptr : backward_side_stream();
+    hipEvent_t fork = nullptr, join = nullptr;
+    if (side != nullptr && hipEventCreateWithFlags(&fork, hipEventDisableTiming) == hipSuccess &&
+        hipEventCreateWithFlags(&join, hipEventDisableTiming) == hipSuccess &&
+        hipEventRecord(fork, st) == hipSuccess && hipStreamWaitEvent(side, fork, 0) == hipSuccess) {
+      hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, side, p);
+      const bool joined = hipEventRecord(join, side) == hipSuccess;
+      hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
+      hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);
+      // join; should that fail, wait for the dV pass on the host instead
+      if (!joined || hipStreamWaitEvent(st, join, 0) != hipSuccess) (void)hipStreamSynchronize(side);
+      (void)hipEventDestroy(join);  // released once the recorded work completes
+      (void)hipEventDestroy(fork);
+      return;
+    }
+    if (fork != nullptr) (void)hipEventDestroy(fork);
+    if (join != nullptr) (void)hipEventDestroy(join);
+    (void)hipGetLastError();  // a failed fork leaves no error behind: run in order below
+  }
+  hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
   if constexpr (FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64) {
     hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, st, p);
     hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);

@@ -160,3 +160,43 @@ def test_forward_fp32_bench_shape_sampled(fa):
         ro, rl = A.prefill_lse(q[sl], k[sl], v[sl], True, compute_dtype=F64)
         assert_close(out.cpu()[sl], ro, atol=2e-4, rtol=2e-4, what="fp32 forward bench shape")
         assert_close(lse.cpu()[sl], rl, atol=2e-4, rtol=2e-4, what="fp32 lse bench shape")
+
+
+def test_backward_concurrent_dv_pass_and_graph_capture(fa):
+    """fp16 D=128: the dV pass runs on a side stream forked from the caller's
+    stream.  Results equal the in-order run under graph capture (where the
+    launches stay on the captured stream) on every replay, and a backward on
+    a non-default stream is ordered with that stream's later work."""
+    g = gen(72)
+    q, k, v, do = (randn(g, 2, 8, 300, 128) for _ in range(4))
+    qc, kc, vc, dc = cuda(q, k, v, do)
+    out, lse = fa.forward_fp16_with_lse(qc, kc, vc, True)
+    eager = fa.backward(dc, qc, kc, vc, out, lse, True)
+    ref = A.backward(do, q, k, v, out.cpu(), lse.cpu(), True)
+    _check_grads(eager, ref, True, "forked dV pass")
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        on_s = fa.backward(dc, qc, kc, vc, out, lse, True)
+        sums = [t.float().sum() for t in on_s]  # consumes the results on the same stream
+    torch.cuda.current_stream().wait_stream(s)
+    for x, y, t in zip(on_s, eager, sums):
+        assert torch.equal(x, y)
+        assert t.item() == y.float().sum().item()
+
+    graph = torch.cuda.CUDAGraph()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fa.backward(dc, qc, kc, vc, out, lse, True)  # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(graph):
+        captured = fa.backward(dc, qc, kc, vc, out, lse, True)
+    for _ in range(3):
+        for t in captured:
+            t.zero_()
+        fa.backward(dc, qc, kc, vc, out, lse, True)  # eager work between the replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for x, y in zip(captured, eager):
+            assert torch.equal(x, y)
