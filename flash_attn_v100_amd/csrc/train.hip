@@ -10,22 +10,22 @@
 namespace fa {
 namespace train {
 
-hipStream_t backward_side_stream() {
+hipStream_t backward_side_stream(int which) {
   constexpr int kMaxDevices = 64;
   static std::mutex mu;
-  static hipStream_t streams[kMaxDevices] = {};
+  static hipStream_t streams[kMaxDevices][2] = {};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (which < 0 || which > 1 || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
-  if (streams[dev] == nullptr) {
+  if (streams[dev][which] == nullptr) {
     hipStream_t s = nullptr;
     if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
       (void)hipGetLastError();  // leave no sticky error for check_launch
       return nullptr;
     }
-    streams[dev] = s;
+    streams[dev][which] = s;
   }
-  return streams[dev];
+  return streams[dev][which];
 }
 
 static int check_sizes(const char* fn, int B, int H, int N, int D) {

@@ -360,6 +360,7 @@ struct TrainParams {
   void* dv;
   float* lse;        // forward: written if non-null; backward: read
   float* delta;      // backward workspace [B*H*N]
+  int delta_ready;   // dQ kernel: delta is already in the workspace (read it, do not recompute)
   int BH, N, D, causal;
   int nblk;          // 128-row blocks per (batch, head)
   float scale;       // 1/sqrt(D)
@@ -502,13 +503,16 @@ __global__ __launch_bounds__(kThreads) void query_major_kernel(TrainParams p) {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       df[kk] = qvalid ? load_frag<T, VEC>(dr, 16 * kk + 8 * hi, D) : zero_frag<T>();
-      const F of = qvalid ? load_frag<T, VEC>(orow, 16 * kk + 8 * hi, D) : zero_frag<T>();
+      if (!p.delta_ready) {
+        const F of = qvalid ? load_frag<T, VEC>(orow, 16 * kk + 8 * hi, D) : zero_frag<T>();
 #pragma unroll
-      for (int j = 0; j < 8; ++j) part = fmaf(static_cast<float>(df[kk][j]), static_cast<float>(of[j]), part);
+        for (int j = 0; j < 8; ++j) part = fmaf(static_cast<float>(df[kk][j]), static_cast<float>(of[j]), part);
+      }
     }
     delta = part + __shfl_xor(part, 32, 64);
     if (qvalid) {
-      if (hi == 0) p.delta[static_cast<size_t>(bh) * N + qrow] = delta;
+      if (p.delta_ready) delta = p.delta[static_cast<size_t>(bh) * N + qrow];  // the same value, from delta_kernel
+      else if (hi == 0) p.delta[static_cast<size_t>(bh) * N + qrow] = delta;
       lse2 = p.lse[static_cast<size_t>(bh) * N + qrow] * kLog2e;
     } else {
       lse2 = INFINITY;  // padding rows: P = 0
@@ -759,14 +763,39 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(TrainParams p) {
     }
 }
 
+// delta_i = sum_d dO[i,d] O[i,d] for every row, into the workspace, with the
+// query-major kernel's exact arithmetic: two fma chains per row, over
+// d = 16 kk + 8 h + j (h = 0, 1; kk = 0 .. DP/16 - 1; j = 0 .. 7; zero past D),
+// then their sum.  Two threads per row.
+template <typename T, int DP, bool VEC>
+__global__ __launch_bounds__(256) void delta_kernel(TrainParams p) {
+  typedef typename Elem<T>::frag F;
+  const long long t = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  const long long rows = static_cast<long long>(p.BH) * p.N;
+  const long long row = min(t >> 1, rows - 1);  // (rows past the end redo the last row, written once)
+  const int h = static_cast<int>(t & 1);
+  const T* dr = static_cast<const T*>(p.dout) + row * p.D;
+  const T* orow = static_cast<const T*>(p.o) + row * p.D;
+  float part = 0.0f;
+#pragma unroll
+  for (int kk = 0; kk < DP / 16; ++kk) {
+    const F df = load_frag<T, VEC>(dr, 16 * kk + 8 * h, p.D);
+    const F of = load_frag<T, VEC>(orow, 16 * kk + 8 * h, p.D);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part = fmaf(static_cast<float>(df[j]), static_cast<float>(of[j]), part);
+  }
+  const float delta = part + __shfl_xor(part, 1, 64);
+  if (h == 0 && (t >> 1) < rows) p.delta[row] = delta;
+}
+
 // ---------------------------------------------------------------------------
 // Launch helpers (the backward is instantiated per element type by train.hip
 // and train_fp32.hip; the fp32 forward, which fits 256 VGPRs, by train.hip).
 
-// A non-blocking, default-priority stream of the current device for the
-// backward's concurrent dV pass (created on first use, kept for the process;
-// nullptr if it cannot be created).  Defined in train.hip.
-hipStream_t backward_side_stream();
+// Non-blocking, default-priority streams (which = 0, 1) of the current
+// device for the backward's concurrent passes (created on first use, kept for
+// the process; nullptr if one cannot be created).  Defined in train.hip.
+hipStream_t backward_side_stream(int which);
 
 template <typename T, int DP, bool VEC>
 void launch_backward_dp(const TrainParams& p, hipStream_t st) {
@@ -776,30 +805,44 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
 #define FA_BWD_SPLIT_DKDV 1
 #endif
   if constexpr (FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64) {
-    // The dV pass needs neither delta nor dQ: it runs on a side stream,
-    // forked from and joined back into `st`, concurrently with the dQ kernel
-    // and the dK pass (each of them leaves most of the MFMA pipe idle).
-    // (not while `st` is being captured into a graph: the capture then keeps
-    // the three launches in order on `st`)
+    // Three concurrent streams: delta (a short kernel) then dQ on `st`, the dK
+    // pass on a side stream once delta is there, and the dV pass, which needs
+    // neither, on another from the start; both join back into `st`.  Each of
+    // the three kernels leaves most of the MFMA pipe idle on its own.  (Not
+    // while `st` is being captured into a graph: the capture then keeps the
+    // launches in order on `st`.)
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(st, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
-    hipStream_t side = capturing ? nullptr : backward_side_stream();
-    hipEvent_t fork = nullptr, join = nullptr;
-    if (side != nullptr && hipEventCreateWithFlags(&fork, hipEventDisableTiming) == hipSuccess &&
-        hipEventCreateWithFlags(&join, hipEventDisableTiming) == hipSuccess &&
-        hipEventRecord(fork, st) == hipSuccess && hipStreamWaitEvent(side, fork, 0) == hipSuccess) {
-      hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, side, p);
-      const bool joined = hipEventRecord(join, side) == hipSuccess;
-      hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
-      hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);
+    hipStream_t side_v = capturing ? nullptr : backward_side_stream(0);
+    hipStream_t side_k = capturing ? nullptr : backward_side_stream(1);
+    hipEvent_t ev[4] = {};  // fork, delta ready, dV done, dK done
+    bool ok = side_v != nullptr && side_k != nullptr;
+    for (int e = 0; ok && e < 4; ++e) ok = hipEventCreateWithFlags(&ev[e], hipEventDisableTiming) == hipSuccess;
+    ok = ok && hipEventRecord(ev[0], st) == hipSuccess && hipStreamWaitEvent(side_v, ev[0], 0) == hipSuccess;
+    if (ok) {
+      hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, side_v, p);
+      const bool v_joined = hipEventRecord(ev[2], side_v) == hipSuccess;
+      const long long rows = static_cast<long long>(p.BH) * p.N;
+      hipLaunchKernelGGL((delta_kernel<T, DP, VEC>), dim3(static_cast<unsigned>((2 * rows + 255) / 256)), dim3(256), 0,
+                         st, p);
+      TrainParams pq = p;
+      pq.delta_ready = 1;
+      bool k_forked = hipEventRecord(ev[1], st) == hipSuccess && hipStreamWaitEvent(side_k, ev[1], 0) == hipSuccess;
+      hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, pq);
+      if (k_forked) {
+        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, side_k, p);
+        if (hipEventRecord(ev[3], side_k) != hipSuccess || hipStreamWaitEvent(st, ev[3], 0) != hipSuccess)
+          (void)hipStreamSynchronize(side_k);
+      } else {
+        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);
+      }
       // join; should that fail, wait for the dV pass on the host instead
-      if (!joined || hipStreamWaitEvent(st, join, 0) != hipSuccess) (void)hipStreamSynchronize(side);
-      (void)hipEventDestroy(join);  // released once the recorded work completes
-      (void)hipEventDestroy(fork);
+      if (!v_joined || hipStreamWaitEvent(st, ev[2], 0) != hipSuccess) (void)hipStreamSynchronize(side_v);
+      for (hipEvent_t e : ev) (void)hipEventDestroy(e);  // released once the recorded work completes
       return;
     }
-    if (fork != nullptr) (void)hipEventDestroy(fork);
-    if (join != nullptr) (void)hipEventDestroy(join);
+    for (hipEvent_t e : ev)
+      if (e != nullptr) (void)hipEventDestroy(e);
     (void)hipGetLastError();  // a failed fork leaves no error behind: run in order below
   }
   hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
