@@ -804,41 +804,47 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
 #ifndef FA_BWD_SPLIT_DKDV
 #define FA_BWD_SPLIT_DKDV 1
 #endif
-  if constexpr (FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64) {
-    // Three concurrent streams: delta (a short kernel) then dQ on `st`, the dK
-    // pass on a side stream once delta is there, and the dV pass, which needs
-    // neither, on another from the start; both join back into `st`.  Each of
-    // the three kernels leaves most of the MFMA pipe idle on its own.  (Not
-    // while `st` is being captured into a graph: the capture then keeps the
-    // launches in order on `st`.)
+  constexpr bool kSplit = FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64;
+  {
+    // Concurrent streams: delta (a short kernel) then dQ on `st`; the dK/dV
+    // pass (or the dK pass) on a side stream once delta is there; with split
+    // passes, the dV pass, which needs neither, on another side stream from
+    // the start.  Everything joins back into `st`.  Each kernel leaves most
+    // of the MFMA pipe idle on its own.  (Not while `st` is being captured
+    // into a graph: the capture then keeps the launches in order on `st`.)
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(st, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
-    hipStream_t side_v = capturing ? nullptr : backward_side_stream(0);
+    hipStream_t side_v = capturing || !kSplit ? nullptr : backward_side_stream(0);
     hipStream_t side_k = capturing ? nullptr : backward_side_stream(1);
-    hipEvent_t ev[4] = {};  // fork, delta ready, dV done, dK done
-    bool ok = side_v != nullptr && side_k != nullptr;
+    hipEvent_t ev[4] = {};  // fork, delta ready, dV done, dK(/dV) done
+    bool ok = side_k != nullptr && (!kSplit || side_v != nullptr);
     for (int e = 0; ok && e < 4; ++e) ok = hipEventCreateWithFlags(&ev[e], hipEventDisableTiming) == hipSuccess;
-    ok = ok && hipEventRecord(ev[0], st) == hipSuccess && hipStreamWaitEvent(side_v, ev[0], 0) == hipSuccess;
+    if (kSplit)
+      ok = ok && hipEventRecord(ev[0], st) == hipSuccess && hipStreamWaitEvent(side_v, ev[0], 0) == hipSuccess;
     if (ok) {
-      hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, side_v, p);
-      const bool v_joined = hipEventRecord(ev[2], side_v) == hipSuccess;
+      bool v_joined = true;
+      if constexpr (kSplit) {
+        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, side_v, p);
+        v_joined = hipEventRecord(ev[2], side_v) == hipSuccess;
+      }
       const long long rows = static_cast<long long>(p.BH) * p.N;
       hipLaunchKernelGGL((delta_kernel<T, DP, VEC>), dim3(static_cast<unsigned>((2 * rows + 255) / 256)), dim3(256), 0,
                          st, p);
       TrainParams pq = p;
       pq.delta_ready = 1;
-      bool k_forked = hipEventRecord(ev[1], st) == hipSuccess && hipStreamWaitEvent(side_k, ev[1], 0) == hipSuccess;
+      const bool k_forked = hipEventRecord(ev[1], st) == hipSuccess && hipStreamWaitEvent(side_k, ev[1], 0) == hipSuccess;
       hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, pq);
-      if (k_forked) {
-        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, side_k, p);
-        if (hipEventRecord(ev[3], side_k) != hipSuccess || hipStreamWaitEvent(st, ev[3], 0) != hipSuccess)
-          (void)hipStreamSynchronize(side_k);
-      } else {
-        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);
-      }
-      // join; should that fail, wait for the dV pass on the host instead
-      if (!v_joined || hipStreamWaitEvent(st, ev[2], 0) != hipSuccess) (void)hipStreamSynchronize(side_v);
-      for (hipEvent_t e : ev) (void)hipEventDestroy(e);  // released once the recorded work completes
+      hipStream_t sk = k_forked ? side_k : st;
+      if constexpr (kSplit)
+        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, sk, p);
+      else
+        hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassBoth>), grid, dim3(kThreads), 0, sk, p);
+      // joins; should one fail, wait for that stream on the host instead
+      if (k_forked && (hipEventRecord(ev[3], side_k) != hipSuccess || hipStreamWaitEvent(st, ev[3], 0) != hipSuccess))
+        (void)hipStreamSynchronize(side_k);
+      if (kSplit && (!v_joined || hipStreamWaitEvent(st, ev[2], 0) != hipSuccess)) (void)hipStreamSynchronize(side_v);
+      for (hipEvent_t e : ev)
+        if (e != nullptr) (void)hipEventDestroy(e);  // released once the recorded work completes
       return;
     }
     for (hipEvent_t e : ev)
@@ -846,7 +852,7 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
     (void)hipGetLastError();  // a failed fork leaves no error behind: run in order below
   }
   hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);
-  if constexpr (FA_BWD_SPLIT_DKDV && sizeof(T) == 2 && DP > 64) {
+  if constexpr (kSplit) {
     hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDV>), grid, dim3(kThreads), 0, st, p);
     hipLaunchKernelGGL((dkdv_kernel<T, DP, VEC, kPassDK>), grid, dim3(kThreads), 0, st, p);
   } else {

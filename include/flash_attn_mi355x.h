@@ -90,9 +90,10 @@ size_t fa_backward_workspace_size(int B, int H, int N);
  * 1 <= D <= 128.  Two or three launches on `stream` (dQ with the row
  * statistic delta = rowsum(dout * out) into the workspace, then dK/dV, as one
  * pass or as a dV and a dK pass); deterministic (no atomics).  The workspace needs no initialisation.
- * fp16 at D > 64 computes delta in a short kernel of its own and runs the dV
- * and dK passes on two library-owned side streams of the device
- * (non-blocking, default priority) concurrently with the dQ kernel, forked
+ * Outside graph capture delta comes from a short kernel of its own and the
+ * dK/dV work (fp16 at D > 64: the dV and the dK pass) runs on library-owned
+ * side streams of the device (non-blocking, default priority) concurrently
+ * with the dQ kernel, forked
  * from `stream` by events and joined back into it before return, so all of
  * the call's work is ordered before later work on `stream`; while `stream`
  * is being captured into a graph every launch stays on `stream`.  Results

@@ -162,18 +162,22 @@ def test_forward_fp32_bench_shape_sampled(fa):
         assert_close(lse.cpu()[sl], rl, atol=2e-4, rtol=2e-4, what="fp32 lse bench shape")
 
 
-def test_backward_concurrent_dv_pass_and_graph_capture(fa):
-    """fp16 D=128: the dV pass runs on a side stream forked from the caller's
-    stream.  Results equal the in-order run under graph capture (where the
-    launches stay on the captured stream) on every replay, and a backward on
-    a non-default stream is ordered with that stream's later work."""
-    g = gen(72)
-    q, k, v, do = (randn(g, 2, 8, 300, 128) for _ in range(4))
+@pytest.mark.parametrize("dtype,d", [(torch.float16, 128), (torch.float16, 64), (torch.float32, 128),
+                                     (torch.float32, 32)])
+def test_backward_concurrent_streams_and_graph_capture(fa, dtype, d):
+    """The backward's kernels run on side streams forked from the caller's
+    stream (delta kernel, dQ, dK/dV passes).  Results equal the in-order run
+    under graph capture (where the launches stay on the captured stream) bit
+    for bit on every replay, and a backward on a non-default stream is
+    ordered with that stream's later work."""
+    g = gen(72 + d)
+    q, k, v, do = (randn(g, 2, 8, 300, d, dtype=dtype) for _ in range(4))
     qc, kc, vc, dc = cuda(q, k, v, do)
-    out, lse = fa.forward_fp16_with_lse(qc, kc, vc, True)
+    fwd = fa.forward_fp16_with_lse if dtype == torch.float16 else fa.forward_with_lse
+    out, lse = fwd(qc, kc, vc, True)
     eager = fa.backward(dc, qc, kc, vc, out, lse, True)
     ref = A.backward(do, q, k, v, out.cpu(), lse.cpu(), True)
-    _check_grads(eager, ref, True, "forked dV pass")
+    _check_grads(eager, ref, dtype == torch.float16, "concurrent backward")
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
