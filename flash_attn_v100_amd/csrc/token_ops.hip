@@ -5,16 +5,16 @@
 // row's attention scores ascending on one thread (swapping only when
 // s[j] > s[j+1], i.e. a stable sort), evicts the `num_evict` lowest, and
 // copies the kept K/V rows, in their original order, to the front of
-// zero-filled outputs.  Here that is two launches:
-//  1. rank_kernel: token i of row b is kept iff its stable ascending rank
-//       #{j : s_j < s_i} + #{j < i : s_j == s_i}
-//     is >= num_evict -- the position the stable sort gives it.  Scores of a
-//     row sit in LDS; 16 lanes share each token's count.
-//  2. compact_kernel: one workgroup per (batch, KV head, block of output rows)
-//     turns the keep mask into the destination -> source row map (a
-//     workgroup prefix count in LDS) and streams its output rows with 16-byte
-//     loads and stores: kept rows copied, the tail zero-filled.  This is the
-//     HBM-bound part: kept rows are read once, every output row written once.
+// zero-filled outputs.  Here that is one launch, one workgroup per (batch,
+// KV head, block of output rows): each derives its batch row's keep mask --
+// token i is kept iff its stable ascending rank
+//     #{j : s_j < s_i} + #{j < i : s_j == s_i}
+// is >= num_evict, the position the stable sort gives it -- from a radix
+// select of the num_evict-th smallest score, turns it into the destination ->
+// source row map (a workgroup prefix count in LDS) and streams its output
+// rows with 16-byte loads and stores: kept rows copied, the tail zero-filled.
+// This is the HBM-bound part: kept rows are read once, every output row
+// written once.
 // Scores containing NaN are outside the contract (the reference's bubble sort
 // then depends on where the NaN sits; the rank order does not).
 #include "capi_internal.h"
@@ -27,70 +27,147 @@ constexpr int kMaxN = 1024;  // the reference's limit (shared arrays of 1024)
 constexpr int kThreads = 256;
 constexpr int kRowsPerBlock = 128;  // output rows per compaction workgroup
 
-// 16 lanes per token: lane g of token i's group counts j = g, g + 16, ...;
-// the 16 partial ranks are summed with DPP moves inside the 16-lane row.
-constexpr int kRankLanes = 16;
-constexpr int kTokensPerBlock = kThreads / kRankLanes;
-__global__ __launch_bounds__(kThreads) void rank_kernel(const float* __restrict__ scores, int32_t* __restrict__ keep,
-                                                       int N, int num_evict) {
-  __shared__ float s[kMaxN];
-  const int b = blockIdx.y;
-  const float* sb = scores + static_cast<size_t>(b) * N;
-  for (int j = threadIdx.x; j < N; j += kThreads) s[j] = sb[j];
-  __syncthreads();
-  const int g = threadIdx.x % kRankLanes;
-  const int i = blockIdx.x * kTokensPerBlock + threadIdx.x / kRankLanes;
-  const int ii = min(i, N - 1);
-  const float si = s[ii];
-  int rank = 0;
-  for (int j = g; j < N; j += kRankLanes) {
-    const float sj = s[j];
-    rank += (sj < si || (sj == si && j < ii)) ? 1 : 0;
-  }
-  rank = group_sum_i<kRankLanes>(rank);
-  if (g == 0 && i < N) keep[static_cast<size_t>(b) * N + i] = rank >= num_evict ? 1 : 0;
-}
-
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void compact_kernel(const half_t* __restrict__ k, const half_t* __restrict__ v,
-                                                          const int32_t* __restrict__ keep, half_t* __restrict__ ko,
-                                                          half_t* __restrict__ vo, int H, int N, int D) {
-  __shared__ int src_of[kMaxN];  // output row -> source row (kept rows only)
-  __shared__ int wave_total[kThreads / 64];
-  const int bh = blockIdx.y;
-  const int b = bh / H;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-
-  // ---- prefix count of kept tokens: thread t owns tokens 4t .. 4t+3 ----
-  const int32_t* kb = keep + static_cast<size_t>(b) * N;
-  int flag[4];
-  int cnt = 0;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int i = 4 * tid + q;
-    flag[q] = (i < N && kb[i] != 0) ? 1 : 0;
-    cnt += flag[q];
-  }
+// Block-wide exclusive prefix count of one flag per token (thread t owns
+// tokens 4t .. 4t+3, in flag[0..3]); returns the count before thread t's first
+// token and sets `total`.  `scratch` holds kThreads / 64 ints.
+__device__ __forceinline__ int block_prefix(const int (&flag)[4], int* scratch, int& total) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cnt = flag[0] + flag[1] + flag[2] + flag[3];
   int incl = cnt;  // inclusive scan over the wave
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
     const int y = __shfl_up(incl, off, 64);
     if (lane >= off) incl += y;
   }
-  if (lane == 63) wave_total[wave] = incl;
+  __syncthreads();  // scratch may still be read by a previous call
+  if (lane == 63) scratch[wave] = incl;
   __syncthreads();
-  int before = 0, kept = 0;
+  int before = 0;
+  total = 0;
 #pragma unroll
   for (int w = 0; w < kThreads / 64; ++w) {
-    before += (w < wave) ? wave_total[w] : 0;
-    kept += wave_total[w];
+    before += (w < wave) ? scratch[w] : 0;
+    total += scratch[w];
   }
-  int dst = before + incl - cnt;
+  return before + incl - cnt;
+}
+
+// Order-preserving unsigned key of a (non-NaN) score: -0.0 and +0.0 compare
+// equal as floats and so map to one key.
+__device__ __forceinline__ uint32_t score_key(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x == 0.0f ? 0.0f : x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// One workgroup per (batch, KV head, block of output rows).  Every workgroup
+// of batch row b derives row b's keep mask itself (1024 scores at most):
+// a radix select (four 8-bit passes over LDS histograms) finds the key T of
+// the num_evict-th smallest score and the count c of smaller ones; a token is
+// evicted iff its key is below T, or equals T and fewer than num_evict - c
+// equal keys precede it -- exactly the tokens whose stable ascending rank
+// #{j : s_j < s_i} + #{j < i : s_j == s_i} is below num_evict, i.e. the first
+// num_evict of the reference's stable sort.  A prefix count of the keep mask
+// then gives the output -> source row map, and the workgroup streams its
+// output rows: kept rows copied, the tail zero-filled.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void evict_kernel(const half_t* __restrict__ k, const half_t* __restrict__ v,
+                                                        const float* __restrict__ scores, int32_t* __restrict__ keep,
+                                                        half_t* __restrict__ ko, half_t* __restrict__ vo, int H,
+                                                        int N, int D, int num_evict) {
+  __shared__ int src_of[kMaxN];  // output row -> source row (kept rows only)
+  __shared__ int hist[256];
+  __shared__ int scratch[kThreads / 64];
+  __shared__ int pick[2];
+  const int bh = blockIdx.y;
+  const int b = bh / H;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  // ---- keys of this thread's tokens 4t .. 4t+3 ----
+  const float* sb = scores + static_cast<size_t>(b) * N;
+  uint32_t key[4];
+  bool valid[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = 4 * tid + q;
+    valid[q] = i < N;
+    key[q] = valid[q] ? score_key(sb[i]) : 0u;
+  }
+  const int E = num_evict;
+  int keepf[4];
+  if (E <= 0 || E >= N) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) keepf[q] = (valid[q] && E <= 0) ? 1 : 0;
+  } else {
+    // ---- radix select of the E-th smallest key (1-based) ----
+    uint32_t prefix = 0u, himask = 0u;
+    int need = E, below = 0;
+#pragma unroll 1
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      hist[tid] = 0;  // kThreads == 256 bins
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (valid[q] && (key[q] & himask) == prefix) atomicAdd(&hist[(key[q] >> shift) & 255u], 1);
+      __syncthreads();
+      if (wave == 0) {
+        int c[4], sum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c[j] = hist[4 * lane + j];
+          sum += c[j];
+        }
+        int incl = sum;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int y = __shfl_up(incl, off, 64);
+          if (lane >= off) incl += y;
+        }
+        int run = incl - sum;  // keys in the bins before this lane's first bin
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // the bin where the running count first reaches `need` (one lane, one j)
+          if (run < need && run + c[j] >= need) {
+            pick[0] = 4 * lane + j;
+            pick[1] = run;
+          }
+          run += c[j];
+        }
+      }
+      __syncthreads();
+      const int digit = pick[0];
+      need -= pick[1];
+      below += pick[1];
+      prefix |= static_cast<uint32_t>(digit) << shift;
+      himask |= 0xFFu << shift;
+      __syncthreads();  // every thread has read pick before the next pass
+    }
+    // prefix = T; below = #{key < T}; the first E - below keys equal to T are evicted
+    int eq[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) eq[q] = (valid[q] && key[q] == prefix) ? 1 : 0;
+    int eq_total;
+    int eq_before = block_prefix(eq, scratch, eq_total);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      keepf[q] = valid[q] && (key[q] > prefix || (eq[q] && eq_before >= E - below)) ? 1 : 0;
+      eq_before += eq[q];
+    }
+  }
+  // the mask output: written once per batch row
+  if (bh % H == 0 && blockIdx.x == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (valid[q]) keep[static_cast<size_t>(b) * N + 4 * tid + q] = keepf[q];
+  }
+
+  // ---- prefix count of kept tokens -> output row map ----
+  int kept;
+  int dst = block_prefix(keepf, scratch, kept);
 #pragma unroll
   for (int q = 0; q < 4; ++q)
-    if (flag[q]) src_of[dst++] = 4 * tid + q;
+    if (keepf[q]) src_of[dst++] = 4 * tid + q;
   __syncthreads();
 
   // ---- output rows [r0, r0 + kRowsPerBlock) of this (batch, head) ----
@@ -359,18 +436,16 @@ extern "C" int fa_token_eviction(const void* k, const void* v, const float* attn
   if (!k || !v || !attn_scores || !k_out || !v_out || !keep_mask)
     return set_error(FA_ERR_INVALID_ARG, "%s: null pointer", fn);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(rank_kernel, dim3(ceil_div(N, kTokensPerBlock), B), dim3(kThreads), 0, st, attn_scores,
-                     keep_mask, N, num_evict);
   const bool vec = D % 8 == 0 && aligned16(k) && aligned16(v) && aligned16(k_out) && aligned16(v_out);
   const dim3 grid(ceil_div(N, kRowsPerBlock), B * H_KV);
   const half_t* kh = static_cast<const half_t*>(k);
   const half_t* vh = static_cast<const half_t*>(v);
   if (vec)
-    hipLaunchKernelGGL(compact_kernel<true>, grid, dim3(kThreads), 0, st, kh, vh, keep_mask,
-                       static_cast<half_t*>(k_out), static_cast<half_t*>(v_out), H_KV, N, D);
+    hipLaunchKernelGGL(evict_kernel<true>, grid, dim3(kThreads), 0, st, kh, vh, attn_scores, keep_mask,
+                       static_cast<half_t*>(k_out), static_cast<half_t*>(v_out), H_KV, N, D, num_evict);
   else
-    hipLaunchKernelGGL(compact_kernel<false>, grid, dim3(kThreads), 0, st, kh, vh, keep_mask,
-                       static_cast<half_t*>(k_out), static_cast<half_t*>(v_out), H_KV, N, D);
+    hipLaunchKernelGGL(evict_kernel<false>, grid, dim3(kThreads), 0, st, kh, vh, attn_scores, keep_mask,
+                       static_cast<half_t*>(k_out), static_cast<half_t*>(v_out), H_KV, N, D, num_evict);
   return check_launch(fn);
 }
 

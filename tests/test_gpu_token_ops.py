@@ -31,6 +31,31 @@ def test_token_eviction(fa, b, h, n, d, num_evict, ties):
     assert torch.equal(vo.cpu(), rv)
 
 
+@pytest.mark.parametrize("pattern", ["signed_zeros", "all_equal", "extremes", "few_distinct"])
+@pytest.mark.parametrize("n,num_evict", [(1024, 1), (1024, 1023), (700, 350), (129, 64)])
+def test_token_eviction_score_patterns(fa, pattern, n, num_evict):
+    """The keep mask comes from a radix select over order-preserving keys:
+    -0.0 and +0.0 tie (stable order decides), equal scores, infinities and
+    values straddling the sign."""
+    g = torch.Generator().manual_seed(n * 7 + num_evict)
+    b, h, d = 2, 3, 64
+    k, v = randn(g, b, h, n, d), randn(g, b, h, n, d)
+    if pattern == "signed_zeros":
+        sc = torch.tensor([0.0, -0.0, 1.0, -1.0])[torch.randint(0, 4, (b, n), generator=g)]
+    elif pattern == "all_equal":
+        sc = torch.full((b, n), -2.5)
+    elif pattern == "extremes":
+        vals = torch.tensor([float("-inf"), -3.4e38, -1e-45, 0.0, 1e-45, 3.4e38, float("inf")])
+        sc = vals[torch.randint(0, vals.numel(), (b, n), generator=g)]
+    else:
+        sc = torch.randint(-2, 3, (b, n), generator=g).float() * 1e-3
+    ko, vo, m = fa.token_eviction(k.cuda(), v.cuda(), sc.cuda(), num_evict)
+    rk, rv, rm = A.token_eviction(k, v, sc, num_evict)
+    assert torch.equal(m.cpu(), rm)
+    assert torch.equal(ko.cpu(), rk)
+    assert torch.equal(vo.cpu(), rv)
+
+
 def test_token_eviction_validation(fa):
     k = torch.zeros(1, 2, 8, 64, dtype=torch.float16, device="cuda")
     sc = torch.zeros(1, 8, device="cuda")
