@@ -286,7 +286,16 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     return (static_cast<size_t>(pg) * p.H_KV + hkv) * kPage * D;
   };
 
-  // ---- query fragments: MFMA A operand, lane holds head l16, columns 32c + 8*q4 .. +8 ----
+  // ---- query fragments: MFMA A operand, lane holds head l16, columns
+  //      k_col(c) .. +8 of slice c (the K fragments use the same columns) ----
+  // The score sums over every column once whatever the order, so the INT8 KV
+  // cache pairs slices (c, c + 1) at 16 contiguous columns 16*q4 + 64*(c/2)
+  // (+8 for c + 1): one 16-byte load of int8 codes per pair.  Other modes:
+  // columns 32c + 8*q4.
+  auto k_col = [&](int c) {
+    if constexpr (MODE == kModeInt8KV && NC % 2 == 0) return 16 * q4 + 64 * (c / 2) + 8 * (c % 2);
+    else return 32 * c + 8 * q4;
+  };
   const int hq_lane = hkv * G + g_base + l16;  // head of this lane's A row
   const bool row_ok = l16 < g_valid;
   half8_t qa[NC];
@@ -309,7 +318,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       u32x4 x = u32x4{0u, 0u, 0u, 0u};
-      if (row_ok) x = load_row8<VEC>(qrow, 32 * c + 8 * q4, D);
+      if (row_ok) x = load_row8<VEC>(qrow, k_col(c), D);
       qa[c] = __builtin_bit_cast(half8_t, x);
       if constexpr (MODE == kModeInt8) quant8(x, inv_qs, qi8[c][0], qi8[c][1]);
     }
@@ -357,8 +366,18 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     for (int tt = 0; tt < T16; ++tt) {
       const int t = min(t0 + 16 * tt + l16, klast);
       T.ks[tt] = p.k_sc[sbase + t];
+      if constexpr (VEC) {
+        // slices c, c + 1 in one 16-byte load (columns k_col(c) .. +16)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) T.k[tt][c] = load_i8x8<VEC>(kh + static_cast<size_t>(t) * D, 32 * c + 8 * q4, D);
+        for (int c = 0; c < NC; c += 2) {
+          const u32x4 x = *reinterpret_cast<const u32x4*>(kh + static_cast<size_t>(t) * D + k_col(c));
+          T.k[tt][c] = u32x2{x[0], x[1]};
+          T.k[tt][c + 1] = u32x2{x[2], x[3]};
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) T.k[tt][c] = load_i8x8<VEC>(kh + static_cast<size_t>(t) * D, k_col(c), D);
+      }
     }
 #pragma unroll
     for (int u = 0; u < UV; ++u) {
@@ -854,7 +873,7 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   }
   // Vector path: D fills the padded width exactly and every row starts 16-byte aligned.
   const bool vec = (p.D == pl.dp) && aligned16(p.q) &&
-                   (MODE == kModeInt8KV ? aligned8(p.k8) && aligned8(p.v8) : aligned16(p.k) && aligned16(p.v));
+                   (MODE == kModeInt8KV ? aligned16(p.k8) && aligned8(p.v8) : aligned16(p.k) && aligned16(p.v));
   const long long units = static_cast<long long>(p.B) * p.H_KV * pl.num_hg;
   hipStream_t st = static_cast<hipStream_t>(stream);
   for (long long u0 = 0; u0 < units; u0 += static_cast<long long>(kCounterSlots)) {

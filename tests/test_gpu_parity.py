@@ -629,6 +629,21 @@ def test_decode_int8_kv_cache(fa, b, hq, hkv, n, d, cache_len):
     assert_close(out, A.decode_int8_kv_cache(q, k8, v8, ks, vs, cache_len), what="int8 kv cache")
 
 
+def test_decode_int8_kv_cache_unaligned_codes(fa):
+    """K codes 8 bytes past a 16-byte boundary: the per-slice load path (the
+    16-byte paired-slice loads need 16-byte-aligned rows)."""
+    g = gen(4242)
+    b, hq, hkv, n, d = 2, 8, 2, 333, 128
+    q = randn(g, b, hq, 1, d)
+    k8, v8, ks, vs = _int8_cache(g, b, hkv, n, d)
+    buf = torch.empty(k8.numel() + 8, dtype=torch.int8, device="cuda")
+    k8u = buf[8:].view(k8.shape)
+    k8u.copy_(k8.cuda())
+    assert k8u.data_ptr() % 16 == 8
+    out = fa.forward_decode_int8_kv_cache_gqa(q.cuda(), k8u, v8.cuda(), ks.cuda(), vs.cuda(), 300)
+    assert_close(out, A.decode_int8_kv_cache(q, k8, v8, ks, vs, 300), what="int8 kv cache, unaligned codes")
+
+
 def test_decode_int8_kv_cache_validation(fa):
     q = torch.zeros(1, 4, 1, 64, dtype=torch.float16, device=DEV)
     k8 = torch.zeros(1, 2, 32, 64, dtype=torch.int8, device=DEV)
