@@ -461,8 +461,8 @@ def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note "
-                                   "(DESIGN.md), not a measured path", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; sharding over several GPUs is a "
+                                   "design, not a measured path", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
