@@ -490,7 +490,7 @@ def main():
         "2": lambda: cfg2_decode(fa, torch, args.steps, args.warmup),
         "3": lambda: cfg3_cb(fa, torch, 30, 5),
         "4": lambda: cfg4_paged(fa, torch, 30, 5),
-        "5a": lambda: cfg5a_varlen(fa, torch, 20, 3),
+        "5a": lambda: cfg5a_varlen(fa, torch, 50, 10),
         "5b": lambda: cfg5b_int8(fa, torch, 100, 10),
         "6a": lambda: cfg6a_int8_kv_cache(fa, torch, 100, 10),
         "6b": lambda: cfg6b_sliding_window(fa, torch, 100, 10),
