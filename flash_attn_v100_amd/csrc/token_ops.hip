@@ -74,6 +74,7 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(const half_t* __restric
                                                         const float* __restrict__ scores, int32_t* __restrict__ keep,
                                                         half_t* __restrict__ ko, half_t* __restrict__ vo, int H,
                                                         int N, int D, int num_evict) {
+  static_assert(kThreads == 256 && 4 * kThreads == kMaxN, "one histogram bin and four tokens per thread");
   __shared__ int src_of[kMaxN];  // output row -> source row (kept rows only)
   __shared__ int hist[256];
   __shared__ int scratch[kThreads / 64];
