@@ -234,7 +234,7 @@ int fa_decode_int8_gqa(const void* q, const void* k, const void* v, void* o,
  * zero.  keep_mask int32 [B, N] receives 1 for kept and 0 for evicted tokens.
  *   k/v/k_out/v_out fp16 [B, H_KV, N, D], attn_scores fp32 [B, N], N <= 1024;
  *   num_evict <= 0 keeps all, >= N drops all.  Scores with NaN are outside
- *   the contract.  Two launches on `stream`.
+ *   the contract.  One launch on `stream`.
  * Replaces token_eviction_forward (flash_attn_kernel.cu:4296-4344), kernel
  * token_eviction_kernel (:4223-4294).
  */
