@@ -27,7 +27,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ["decode.hip", "prefill.hip", "train.hip", "train_fp32.hip", "token_ops.hip"]
+KERNEL_SOURCES = ["decode.hip", "prefill.hip", "train.hip", "train_fp32.hip", "token_ops.hip", "tp_ops.hip"]
 HOST_SOURCES = ["capi.cpp"]
 
 HIP_FLAGS = [

@@ -6,7 +6,6 @@
 // validation (same conditions, same messages, raised as RuntimeError through
 // TORCH_CHECK) and its output contract, then calls one fa_* entry point on the
 // caller's current HIP stream (the `_stream` variants: on the given stream).
-// Names the MI355X build does not implement raise RuntimeError.
 #include <torch/extension.h>
 
 #include <ATen/hip/impl/HIPCachingAllocatorMasqueradingAsCUDA.h>
@@ -14,7 +13,6 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <cmath>
-#include <unordered_map>
 #include <tuple>
 #include <vector>
 
@@ -145,34 +143,84 @@ void check_prefill_gqa_output_tensor(const at::Tensor& out, const at::Tensor& q)
   TORCH_CHECK(out.sizes() == q.sizes(), "out shape must match q shape for prefill mode");
 }
 
-// Split-KV workspace: one zero-filled buffer per (device, stream), grown on
-// demand and kept for the life of the process.  The kernels leave its arrival
-// counters at zero after every call, and calls on one stream run in order, so
-// the buffer never needs clearing again.  Distinct streams get distinct buffers,
-// so concurrent calls never share counters.  (The GIL serialises this map.)
-struct WorkspaceKey {
+// Split-KV workspace.  The kernels leave its arrival counters at zero after
+// every call, so a buffer is zero-filled once, when allocated, and then serves
+// any number of calls issued in order on one stream.  Two pools:
+//  * eager calls: one buffer per (device, stream), least recently used first
+//    out once a device holds kMaxEagerWorkspaces of them (a server that makes
+//    a stream per request does not accumulate buffers).  A dropped or
+//    outgrown buffer returns to the caching allocator, which hands it only to
+//    later allocations on the same stream, i.e. after the calls already queued
+//    there.
+//  * calls under graph capture: one buffer per (device, capturing stream),
+//    never shared with eager calls and never released: a captured graph keeps
+//    the buffer's address, so an outgrown one is retired but kept alive.
+//    Graphs captured on one stream share that buffer and must be replayed in
+//    order, not concurrently with each other.
+// The GIL serialises every use of these pools.
+constexpr size_t kMaxEagerWorkspaces = 8;
+
+struct WorkspaceEntry {
   int device;
   uintptr_t stream;
-  bool operator==(const WorkspaceKey& o) const { return device == o.device && stream == o.stream; }
+  at::Tensor buf;
+  uint64_t last_use;
 };
-struct WorkspaceKeyHash {
-  size_t operator()(const WorkspaceKey& k) const { return std::hash<uintptr_t>()(k.stream) ^ (size_t)k.device; }
+
+struct WorkspacePools {
+  std::vector<WorkspaceEntry> eager;
+  std::vector<WorkspaceEntry> captured;
+  std::vector<at::Tensor> retired;  // outgrown capture buffers, still referenced by graphs
+  uint64_t tick = 0;
 };
+
+bool stream_is_capturing(void* stream) {
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  const hipError_t err = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &status);
+  TORCH_CHECK(err == hipSuccess, "hipStreamIsCapturing: ", hipGetErrorString(err));
+  return status != hipStreamCaptureStatusNone;
+}
 
 at::Tensor decode_workspace(const at::Tensor& q, int B, int H_Q, int H_KV, int max_len, int D) {
   // Deliberately leaked: destroying tensors after the HIP runtime shut down at exit is unsafe.
-  static auto& cache = *new std::unordered_map<WorkspaceKey, at::Tensor, WorkspaceKeyHash>();
+  static auto& pools = *new WorkspacePools();
   const size_t bytes = fa_decode_workspace_size(B, H_Q, H_KV, max_len, D);
   if (bytes == 0) return at::Tensor();
-  const WorkspaceKey key{q.device().index(), reinterpret_cast<uintptr_t>(cur_stream())};
-  auto it = cache.find(key);
-  if (it != cache.end() && static_cast<size_t>(it->second.numel()) >= bytes) return it->second;
-  // Grow geometrically; the old buffer returns to the caching allocator, which
-  // reuses it only for work ordered after the calls already queued on this stream.
-  size_t alloc = bytes;
-  if (it != cache.end()) alloc = std::max(bytes, static_cast<size_t>(it->second.numel()) * 2);
-  at::Tensor ws = at::zeros({static_cast<int64_t>(alloc)}, q.options().dtype(at::kByte));
-  cache[key] = ws;
+  void* stream = cur_stream();
+  const int device = q.device().index();
+  const uintptr_t sid = reinterpret_cast<uintptr_t>(stream);
+  const bool capturing = stream_is_capturing(stream);
+  auto& pool = capturing ? pools.captured : pools.eager;
+  const uint64_t now = ++pools.tick;
+  for (auto& e : pool) {
+    if (e.device != device || e.stream != sid) continue;
+    if (static_cast<size_t>(e.buf.numel()) >= bytes) {
+      e.last_use = now;
+      return e.buf;
+    }
+    // Grow geometrically.
+    const size_t alloc = std::max(bytes, static_cast<size_t>(e.buf.numel()) * 2);
+    at::Tensor grown = at::zeros({static_cast<int64_t>(alloc)}, q.options().dtype(at::kByte));
+    if (capturing) pools.retired.push_back(e.buf);
+    e.buf = grown;
+    e.last_use = now;
+    return grown;
+  }
+  if (!capturing) {
+    size_t on_device = 0;
+    WorkspaceEntry* lru = nullptr;
+    for (auto& e : pool) {
+      if (e.device != device) continue;
+      ++on_device;
+      if (!lru || e.last_use < lru->last_use) lru = &e;
+    }
+    if (on_device >= kMaxEagerWorkspaces && lru) {
+      *lru = pool.back();
+      pool.pop_back();
+    }
+  }
+  at::Tensor ws = at::zeros({static_cast<int64_t>(bytes)}, q.options().dtype(at::kByte));
+  pool.push_back(WorkspaceEntry{device, sid, ws, now});
   return ws;
 }
 
@@ -659,13 +707,59 @@ std::tuple<at::Tensor, at::Tensor> speculative_verify(at::Tensor target_probs, a
 }
 
 // ---------------------------------------------------------------------------
-// Names of the reference module that are outside the MI355X hot path.
+// Tensor-parallel helpers: same-device head-range copies and the fp16 accumulate.
 
-void not_implemented(const char* name) {
-  TORCH_CHECK(false, "flash_attn_v100.", name,
-              " is not implemented in the MI355X build (hot path: forward_fp16, forward_fp16_wmma, "
-              "forward_decode_fp16, forward_decode_gqa_fp16, forward_continuous_batching_fp16, "
-              "forward_varlen_prefill_fp16, forward_paged_decode_gqa_fp16, forward_decode_int8_gqa)");
+// cross_gpu_allreduce_fp16 (flash_attn_kernel.cu:597-620)
+void cross_gpu_allreduce_fp16(at::Tensor dst_tensor, at::Tensor src_tensor) {
+  CHECK_INPUT(dst_tensor);
+  CHECK_INPUT(src_tensor);
+  TORCH_CHECK(dst_tensor.dtype() == at::kHalf, "dst must be float16");
+  TORCH_CHECK(src_tensor.dtype() == at::kHalf, "src must be float16");
+  TORCH_CHECK(dst_tensor.numel() == src_tensor.numel(), "size mismatch");
+  CHECK_SAME_DEVICE(dst_tensor, src_tensor);
+  HIPGuardMasqueradingAsCUDA guard(dst_tensor.device());
+  check_fa(fa_cross_gpu_allreduce_fp16(dst_tensor.data_ptr(), src_tensor.data_ptr(),
+                                       static_cast<size_t>(dst_tensor.numel()), cur_stream()));
+}
+
+// Shared checks of scatter_heads_forward / gather_heads_forward
+// (flash_attn_kernel.cu:685-701, :728-744).
+void check_head_range(const at::Tensor& full_tensor, const at::Tensor& local_tensor, int total_heads,
+                      int local_head_start, int local_head_count) {
+  CHECK_INPUT(full_tensor);
+  CHECK_INPUT(local_tensor);
+  TORCH_CHECK(full_tensor.dtype() == at::kHalf, "full_tensor must be float16");
+  TORCH_CHECK(local_tensor.dtype() == at::kHalf, "local_tensor must be float16");
+  CHECK_DIM(full_tensor, 4);
+  CHECK_DIM(local_tensor, 4);
+  CHECK_SAME_DEVICE(full_tensor, local_tensor);
+  const auto B = full_tensor.size(0), N = full_tensor.size(2), D = full_tensor.size(3);
+  TORCH_CHECK(full_tensor.size(1) == total_heads, "full_tensor head count must match total_heads");
+  TORCH_CHECK(local_tensor.size(1) == local_head_count, "local_tensor head count must match local_head_count");
+  TORCH_CHECK(local_head_start >= 0 && local_head_count >= 0, "head range must be non-negative");
+  TORCH_CHECK(local_head_start + local_head_count <= total_heads, "head range exceeds total_heads");
+  TORCH_CHECK(local_tensor.size(0) == B && local_tensor.size(2) == N && local_tensor.size(3) == D,
+              "local_tensor shape must match full_tensor except for head count");
+}
+
+// scatter_heads_forward (flash_attn_kernel.cu:678-719)
+void scatter_heads(at::Tensor full_tensor, at::Tensor local_tensor, int total_heads, int local_head_start,
+                   int local_head_count) {
+  check_head_range(full_tensor, local_tensor, total_heads, local_head_start, local_head_count);
+  HIPGuardMasqueradingAsCUDA guard(full_tensor.device());
+  check_fa(fa_scatter_heads(full_tensor.data_ptr(), local_tensor.data_ptr(), to_int(full_tensor.size(0), "B"),
+                            total_heads, local_head_start, local_head_count, to_int(full_tensor.size(2), "N"),
+                            to_int(full_tensor.size(3), "D"), cur_stream()));
+}
+
+// gather_heads_forward (flash_attn_kernel.cu:721-762)
+void gather_heads(at::Tensor full_tensor, at::Tensor local_tensor, int total_heads, int local_head_start,
+                  int local_head_count) {
+  check_head_range(full_tensor, local_tensor, total_heads, local_head_start, local_head_count);
+  HIPGuardMasqueradingAsCUDA guard(full_tensor.device());
+  check_fa(fa_gather_heads(full_tensor.data_ptr(), local_tensor.data_ptr(), to_int(full_tensor.size(0), "B"),
+                           total_heads, local_head_start, local_head_count, to_int(full_tensor.size(2), "N"),
+                           to_int(full_tensor.size(3), "D"), cur_stream()));
 }
 
 // forward_decode_int8_kv_cache_gqa (flash_attn_kernel.cu:4161-4221)
@@ -856,10 +950,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("backward", &backward, "Attention backward for MHA, fp32/fp16 (MI355X MFMA)");
   m.def("token_eviction", &token_eviction, "KV-cache token eviction by attention score (MI355X)");
   m.def("speculative_verify", &speculative_verify, "Speculative decoding verify (MI355X)");
-  for (const char* name : {"cross_gpu_allreduce_fp16", "scatter_heads",
-                           "gather_heads"}) {
-    std::string n(name);
-    m.def(name, [n](pybind11::args, pybind11::kwargs) { not_implemented(n.c_str()); }, "Not implemented on MI355X");
-  }
+  m.def("cross_gpu_allreduce_fp16", &cross_gpu_allreduce_fp16, "fp16 dst += src on one device (MI355X)");
+  m.def("scatter_heads", &scatter_heads, "Copy a head range of full into local (MI355X)");
+  m.def("gather_heads", &gather_heads, "Copy local into a head range of full (MI355X)");
   m.def("_fa_version", []() { return std::string(fa_version()); });
 }

@@ -237,7 +237,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   const int k0 = split * p.chunk;
   // With absorb_tail (fixed-length calls only) the last split also takes the
   // short remainder past (S - 1) * chunk; it stays within kMaxChunk keys.
-  const int k1 = (p.absorb_tail && split == S - 1) ? L : min(L, k0 + p.chunk);
+  // Paged: the splits are planned over the table row (16 * max_num_blocks
+  // tokens); a longer sequence keeps reading the flat table past its row, as
+  // the reference does, and the last split takes all of those keys.
+  const bool last_takes_rest = (p.absorb_tail || MODE == kModePaged) && split == S - 1;
+  const int k1 = last_takes_rest ? L : min(L, k0 + p.chunk);
 
   if (k0 >= k1) {
     // No key at all (L <= 0): the reference's acc/l_i is 0/0 there.  Split 0
@@ -254,15 +258,19 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     return;
   }
 
+  // Paged: the page ids of the keys [r0, r1) being walked are staged in LDS,
+  // kMaxChunk keys per round (one round unless the sequence overruns its
+  // table row).  Token t's page id is block_table.flat[b * max_num_blocks +
+  // t / 16] (flash_attn_kernel.cu:3438); a flat index past the table or a page
+  // id outside [0, num_pages) would be an out-of-bounds read in the reference
+  // and makes this sequence NaN instead.
   __shared__ int s_pages[MODE == kModePaged ? kMaxChunk / kPage : 1];
   __shared__ int s_bad;
-  if constexpr (MODE == kModePaged) {
-    // A sequence longer than its table row would read the next row's page ids.
-    if (tid == 0) s_bad = static_cast<long long>(L) > static_cast<long long>(p.max_num_blocks) * kPage;
-    __syncthreads();
-    const int np = (k1 - k0 + kPage - 1) / kPage;
+  int r0 = k0, npages = 1;
+  auto stage_pages = [&](int from, int to) {
+    const int np = (to - from + kPage - 1) / kPage;
     for (int i = tid; i < np; i += kDecThreads) {
-      const long long idx = static_cast<long long>(b) * p.max_num_blocks + k0 / kPage + i;
+      const long long idx = static_cast<long long>(b) * p.max_num_blocks + from / kPage + i;
       int id = (idx >= 0 && idx < p.bt_numel) ? p.block_table[idx] : -1;
       if (id < 0 || id >= p.num_pages) {
         s_bad = 1;
@@ -271,17 +279,22 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
       s_pages[i] = id;
     }
     __syncthreads();
+    r0 = from;
+    npages = np;
+  };
+  if constexpr (MODE == kModePaged) {
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
   }
 
   // Row addressing.  Contiguous caches: one base per (b, h_kv) plus a 32-bit row
   // offset.  Paged cache: a 16-key MFMA tile and each row-layout load both lie
   // inside one page, so the page base is wave-uniform; rows past k1 inside the
   // last page are real page memory (their scores are masked), and page slots
-  // past the split's last page are clamped to it.
+  // past the round's last page are clamped to it.
   const size_t kv_head_base = (static_cast<size_t>(b) * p.H_KV + hkv) * static_cast<size_t>(p.N) * D;
-  const int npages = (k1 - k0 + kPage - 1) / kPage;
-  auto page_base = [&](int t) -> size_t {  // t: any key of the page, t >= k0
-    const int slot = min((t - k0) >> 4, npages - 1);
+  auto page_base = [&](int t) -> size_t {  // t: any key of the page, t >= r0
+    const int slot = min((t - r0) >> 4, npages - 1);
     const int pg = __builtin_amdgcn_readfirstlane(s_pages[slot]);
     return (static_cast<size_t>(pg) * p.H_KV + hkv) * kPage * D;
   };
@@ -548,7 +561,14 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   };
 
   const int stride = kDecWaves * TK;
-  for (int t0 = k0 + wave * TK; t0 < k1; t0 += stride) {
+  static_assert(kMaxChunk % (kDecWaves * 32) == 0, "page rounds hold whole wave iterations");
+  for (int rb = k0; rb < k1; rb += kMaxChunk) {
+  const int re = (MODE == kModePaged && k1 - rb > kMaxChunk) ? rb + kMaxChunk : k1;
+  if constexpr (MODE == kModePaged) {
+    if (rb != k0) __syncthreads();  // every wave is done with the previous round's ids
+    stage_pages(rb, re);
+  }
+  for (int t0 = rb + wave * TK; t0 < re; t0 += stride) {
     Tile A;
     if constexpr (MODE == kModeInt8KV) {
       Tile8 R;
@@ -563,6 +583,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
       load_tile(A, t0);
     }
     compute_tile(A, t0);
+  }
+  if constexpr (MODE != kModePaged) break;  // contiguous modes: one pass over [k0, k1)
   }
 
   // ---- wave-level reduction: all lanes of a wave share mu, so plain sums ----
@@ -992,9 +1014,8 @@ extern "C" int fa_paged_decode_gqa_fp16(const void* q, const void* k_cache, cons
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = 0; p.D = D;
   p.max_num_blocks = max_num_blocks;
   p.num_pages = num_pages;
-  // Splits cover tokens [0, 16*max_num_blocks); a sequence longer than its
-  // table row is reported as NaN by the last split (the reference would read
-  // the next row's page ids there).
+  // Splits are planned over tokens [0, 16*max_num_blocks); the last split also
+  // takes the tokens of a sequence that overruns its table row.
   const int plan_len = max_len_ll > 0 ? static_cast<int>(max_len_ll) : 1;
   return run_decode<kModePaged>(fn, p, plan_len, workspace, workspace_bytes, stream);
 }

@@ -28,6 +28,22 @@ hipStream_t backward_side_stream(int which) {
   return streams[dev][which];
 }
 
+bool backward_events(hipEvent_t (&ev)[4]) {
+  constexpr int kMaxDevices = 64;
+  thread_local hipEvent_t events[kMaxDevices][4] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  for (int e = 0; e < 4; ++e) {
+    if (events[dev][e] == nullptr &&
+        hipEventCreateWithFlags(&events[dev][e], hipEventDisableTiming) != hipSuccess) {
+      events[dev][e] = nullptr;
+      return false;
+    }
+    ev[e] = events[dev][e];
+  }
+  return true;
+}
+
 static int check_sizes(const char* fn, int B, int H, int N, int D) {
   if (B < 0 || H <= 0 || N < 0 || D <= 0)
     return set_error(FA_ERR_INVALID_ARG, "%s: bad sizes (B=%d H=%d N=%d D=%d)", fn, B, H, N, D);

@@ -678,7 +678,11 @@ __global__ __launch_bounds__(kThreads) void dkdv_kernel(TrainParams p) {
   // causal waves start at the tile holding query wk0
   const int c_begin = wk0 >= N ? ntiles : (p.causal ? (wk0 - qstart) / kRows : 0);  // no keys: no compute
   // (the register-staged fp32 pass measured no gain from it)
-  run_ring<Ring, DMA, VEC, FA_BWD_REV != 0 && DMA>(ring, qp, dop, lse, dlt, qstart, ntiles, c_begin, ntiles, N, D, [&](int stage, int t) {
+  // The dV pass never reads delta, and runs concurrently with the kernel that
+  // writes it: its second per-row stream is pointed at lse instead (staged,
+  // never used), so it touches nothing that kernel writes.
+  const float* __restrict__ vb_rows = DO_DK ? dlt : lse;
+  run_ring<Ring, DMA, VEC, FA_BWD_REV != 0 && DMA>(ring, qp, dop, lse, vb_rows, qstart, ntiles, c_begin, ntiles, N, D, [&](int stage, int t) {
     const int qt = qstart + t * kRows;
     const unsigned qs = ring.addr_a(stage);
     const unsigned ds = ring.addr_b(stage);
@@ -796,6 +800,10 @@ __global__ __launch_bounds__(256) void delta_kernel(TrainParams p) {
 // device for the backward's concurrent passes (created on first use, kept for
 // the process; nullptr if one cannot be created).  Defined in train.hip.
 hipStream_t backward_side_stream(int which);
+// The calling thread's four fork/join events for the current device (created
+// once, reused by every later backward call of that thread); false if they
+// cannot be made.
+bool backward_events(hipEvent_t (&ev)[4]);
 
 template <typename T, int DP, bool VEC>
 void launch_backward_dp(const TrainParams& p, hipStream_t st) {
@@ -817,8 +825,7 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
     hipStream_t side_v = capturing || !kSplit ? nullptr : backward_side_stream(0);
     hipStream_t side_k = capturing ? nullptr : backward_side_stream(1);
     hipEvent_t ev[4] = {};  // fork, delta ready, dV done, dK(/dV) done
-    bool ok = side_k != nullptr && (!kSplit || side_v != nullptr);
-    for (int e = 0; ok && e < 4; ++e) ok = hipEventCreateWithFlags(&ev[e], hipEventDisableTiming) == hipSuccess;
+    bool ok = side_k != nullptr && (!kSplit || side_v != nullptr) && backward_events(ev);
     if (kSplit)
       ok = ok && hipEventRecord(ev[0], st) == hipSuccess && hipStreamWaitEvent(side_v, ev[0], 0) == hipSuccess;
     if (ok) {
@@ -843,12 +850,8 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
       if (k_forked && (hipEventRecord(ev[3], side_k) != hipSuccess || hipStreamWaitEvent(st, ev[3], 0) != hipSuccess))
         (void)hipStreamSynchronize(side_k);
       if (kSplit && (!v_joined || hipStreamWaitEvent(st, ev[2], 0) != hipSuccess)) (void)hipStreamSynchronize(side_v);
-      for (hipEvent_t e : ev)
-        if (e != nullptr) (void)hipEventDestroy(e);  // released once the recorded work completes
       return;
     }
-    for (hipEvent_t e : ev)
-      if (e != nullptr) (void)hipEventDestroy(e);
     (void)hipGetLastError();  // a failed fork leaves no error behind: run in order below
   }
   hipLaunchKernelGGL((query_major_kernel<T, DP, VEC, 1>), grid, dim3(kThreads), 0, st, p);

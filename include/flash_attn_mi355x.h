@@ -196,10 +196,11 @@ int fa_continuous_batching_fp16(const void* q, const void* k, const void* v,
  *   block_table int32 (device), read as flat[b * max_num_blocks + t / 16] for
  *   token t (block_table_numel bounds that read); seq_lens int32 [B] (device).
  *   Sequence b attends tokens [0, seq_lens[b]).  seq_lens[b] <= 0 yields NaN
- *   (0/0, as in the reference).  A page id outside [0, num_pages), a table
- *   index past block_table_numel or seq_lens[b] > 16 * max_num_blocks also
- *   yields NaN for that sequence; the reference reads out of bounds or into the
- *   next table row there.
+ *   (0/0, as in the reference).  A sequence longer than 16 * max_num_blocks
+ *   reads on into the next table row, exactly as the reference's flat read
+ *   does.  A page id outside [0, num_pages) or a table index past
+ *   block_table_numel yields NaN for that sequence (the reference reads out of
+ *   bounds there).
  * Replaces the launch in flash_attn_forward_paged_decode_gqa_fp16
  * (flash_attn_kernel.cu:3516-3584).
  */
@@ -260,6 +261,35 @@ int fa_speculative_verify(const float* target_probs, const float* draft_probs,
                           const int64_t* draft_tokens, const float* random_vals,
                           int32_t* accepted_count, int64_t* output_tokens, int B,
                           int K, int vocab_size, void* stream);
+
+/*
+ * Tensor-parallel head-range copies (same device).
+ *   full fp16 [B, total_heads, N, D], local fp16 [B, head_count, N, D];
+ *   0 <= head_start, 0 <= head_count, head_start + head_count <= total_heads.
+ *   fa_scatter_heads: local[b, h] = full[b, head_start + h];
+ *   fa_gather_heads:  full[b, head_start + h] = local[b, h] (other heads of
+ *   full untouched).  An empty range (head_count, B, N or D zero) is a no-op.
+ * Replace scatter_heads_forward (flash_attn_kernel.cu:678-719, kernel
+ * scatter_heads_kernel :622-648) and gather_heads_forward (:721-762, kernel
+ * gather_heads_kernel :650-676).
+ */
+int fa_scatter_heads(const void* full, void* local, int B, int total_heads,
+                     int head_start, int head_count, int N, int D,
+                     void* stream);
+int fa_gather_heads(void* full, const void* local, int B, int total_heads,
+                    int head_start, int head_count, int N, int D,
+                    void* stream);
+
+/*
+ * fp16 accumulate of the tensor-parallel all-reduce (same device):
+ *   dst[i] = half(float(dst[i]) + float(src[i])) for i < n, rounded to nearest
+ *   even once; src == dst doubles dst; partially overlapping buffers are
+ *   outside the contract.
+ * Replaces cross_gpu_allreduce_fp16 (flash_attn_kernel.cu:597-620, kernel
+ * cross_gpu_reduce_kernel :586-595).
+ */
+int fa_cross_gpu_allreduce_fp16(void* dst, const void* src, size_t n,
+                                void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -490,3 +490,61 @@ def speculative_verify(target_probs, draft_probs, draft_tokens, random_vals, K: 
             out[b, K] = _first_index_quirk(cs >= rv[b, K - 1])
         accepted[b] = acc
     return torch.from_numpy(accepted), torch.from_numpy(out)
+
+
+def _head_range_index(B: int, total_heads: int, head_start: int, head_count: int, N: int, D: int):
+    """Flat (local_idx, full_idx) pairs of the reference's per-element index map
+    (flash_attn_kernel.cu:632-647 scatter, :660-675 gather): element ``idx`` of
+    the local tensor is ``b = idx // (count*N*D)``, ``local_h = rem1 // (N*D)``,
+    ``rem2 = rem1 % (N*D)`` and maps to ``full_idx = b*total*N*D +
+    (local_h + start)*N*D + rem2`` when ``local_h + start < total``."""
+    import numpy as np
+
+    eph = N * D
+    n_local = B * head_count * eph
+    idx = np.arange(n_local, dtype=np.int64)
+    if n_local == 0:
+        return idx, idx
+    b = idx // (head_count * eph)
+    rem1 = idx % (head_count * eph)
+    local_h = rem1 // eph
+    rem2 = rem1 % eph
+    global_h = local_h + head_start
+    keep = global_h < total_heads
+    full_idx = b * total_heads * eph + global_h * eph + rem2
+    return idx[keep], full_idx[keep]
+
+
+def scatter_heads(full, local, total_heads: int, head_start: int, head_count: int):
+    """``scatter_heads`` (flash_attn_kernel.cu:622-648, :678-719): returns the new
+    ``local`` with ``local.flat[idx] = full.flat[full_idx]`` over the reference's
+    index map; elements the map does not reach keep their value."""
+    B, _, N, D = full.shape
+    li, fi = _head_range_index(B, total_heads, head_start, head_count, N, D)
+    out = local.detach().cpu().clone().reshape(-1)
+    out[torch.from_numpy(li)] = full.detach().cpu().reshape(-1)[torch.from_numpy(fi)]
+    return out.reshape(local.shape)
+
+
+def gather_heads(full, local, total_heads: int, head_start: int, head_count: int):
+    """``gather_heads`` (flash_attn_kernel.cu:650-676, :721-762): returns the new
+    ``full`` with ``full.flat[full_idx] = local.flat[idx]``; other heads untouched."""
+    B, _, N, D = full.shape
+    li, fi = _head_range_index(B, total_heads, head_start, head_count, N, D)
+    out = full.detach().cpu().clone().reshape(-1)
+    out[torch.from_numpy(fi)] = local.detach().cpu().reshape(-1)[torch.from_numpy(li)]
+    return out.reshape(full.shape)
+
+
+def allreduce_fp16(dst, src):
+    """``cross_gpu_allreduce_fp16`` (flash_attn_kernel.cu:586-595, :597-620):
+    ``dst[i] = __float2half(__half2float(dst[i]) + __half2float(src[i]))`` --
+    widen, one fp32 add (round to nearest even), one narrowing (round to nearest
+    even).  Returns the new dst."""
+    import numpy as np
+
+    a = dst.detach().cpu().numpy().astype(np.float16).astype(np.float32)
+    b = src.detach().cpu().numpy().astype(np.float16).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        s = (a + b).astype(np.float32).astype(np.float16)
+    return torch.from_numpy(s).reshape(dst.shape)

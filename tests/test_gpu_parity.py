@@ -175,14 +175,40 @@ def test_decode_workspace_shared_across_shapes(fa):
         assert_close(out, A.decode_int8(*b, qs, ks, 1024), what="int8 after small-unit call")
 
 
-def test_paged_decode_sequence_longer_than_table_row_is_nan(fa):
+def test_paged_decode_sequence_longer_than_table_row_reads_on(fa):
+    """A sequence longer than 16 * max_num_blocks keeps reading the flattened
+    table past its own row (flash_attn_kernel.cu:3438), as the reference does."""
     g = gen(22)
     q, kc, vc = randn(g, 2, 4, 1, 64), randn(g, 8, 2, 16, 64), randn(g, 8, 2, 16, 64)
     bt = torch.tensor([[0, 1], [2, 3]], dtype=torch.int32)
-    slt = torch.tensor([40, 20], dtype=torch.int32)  # 40 > 16 * max_num_blocks
+    slt = torch.tensor([40, 20], dtype=torch.int32)  # 40 > 16 * max_num_blocks: row 0 reads page 2 too
     out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), 2)
-    assert torch.isnan(out[0].float()).all()
-    assert_close(out[1:], A.paged_decode(q[1:], kc, vc, bt[1:], slt[1:], 2), what="paged row 1")
+    assert_close(out, A.paged_decode(q, kc, vc, bt, slt, 2), what="paged overrun")
+
+
+def test_paged_decode_overrun_spanning_page_rounds(fa):
+    """An overrun far past the row (17 600 tokens on a 10-block row stride) is
+    walked by the last split in several rounds of staged page ids."""
+    g = gen(24)
+    B, Hq, Hkv, D, P = 2, 8, 2, 64, 64
+    q, kc, vc = randn(g, B, Hq, 1, D), randn(g, P, Hkv, 16, D), randn(g, P, Hkv, 16, D)
+    bt = torch.randint(0, P, (B, 600), generator=g, dtype=torch.int32)
+    slt = torch.tensor([16 * 1100, 150], dtype=torch.int32)
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), 10)
+    assert_close(out, A.paged_decode(q, kc, vc, bt, slt, 10), what="paged multi-round overrun")
+
+
+def test_paged_decode_out_of_bounds_reads_are_nan(fa):
+    """Only genuinely out-of-bounds reads (a flat table index past
+    block_table.numel(), a page id outside [0, num_pages)) give NaN, and only
+    for the sequence that makes them."""
+    g = gen(25)
+    q, kc, vc = randn(g, 3, 4, 1, 64), randn(g, 8, 2, 16, 64), randn(g, 8, 2, 16, 64)
+    bt = torch.tensor([[0, 1], [2, 3], [4, 9]], dtype=torch.int32)  # page 9 >= num_pages
+    slt = torch.tensor([20, 70, 30], dtype=torch.int32)  # row 1: 70 tokens need flat index 6 >= numel 6
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), 2)
+    assert torch.isnan(out[1:].float()).all()
+    assert_close(out[:1], A.paged_decode(q[:1], kc, vc, bt, slt[:1], 2), what="paged row 0")
 
 
 def test_decode_gqa_out_and_stream(fa):
@@ -567,6 +593,62 @@ def test_decode_graph_capture_replays(fa):
         for o, e, r in zip(outs, eager, refs):
             assert torch.equal(o, e)
             assert_close(o, r, what="graph replay")
+
+
+def test_decode_graph_survives_workspace_growth_on_its_stream(fa):
+    """Capture on a stream, then make a larger eager decode call on that same
+    stream (which grows the eager workspace) and allocate more memory: the
+    captured graph keeps its own workspace, so every replay still matches the
+    eager result and the new allocations keep their contents."""
+    g = gen(10)
+    small = (randn(g, 1, 32, 1, 128), randn(g, 1, 8, 1025, 128), randn(g, 1, 8, 1025, 128))
+    big = (randn(g, 4, 32, 1, 128), randn(g, 4, 8, 16385, 128), randn(g, 4, 8, 16385, 128))
+    sd, bd = cuda(*small), cuda(*big)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        fa.forward_decode_gqa_fp16(*sd, True, 1024)
+    st.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        out = fa.forward_decode_gqa_fp16(*sd, True, 1024)
+    ref_small = A.decode(*small, True, 1024)
+    with torch.cuda.stream(st):
+        big_out = fa.forward_decode_gqa_fp16(*bd, True, 16384)  # grows the eager workspace of st
+        filler = [torch.full((1 << 20,), float(i), device="cuda") for i in range(8)]
+    st.synchronize()
+    ref_big = A.decode(*big, True, 16384)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert_close(out, ref_small, what="graph replay after growth")
+        with torch.cuda.stream(st):
+            again = fa.forward_decode_gqa_fp16(*bd, True, 16384)
+        st.synchronize()
+        assert torch.equal(again, big_out)
+    assert_close(big_out, ref_big, what="grown eager call")
+    for i, f in enumerate(filler):
+        assert torch.equal(f, torch.full_like(f, float(i)))
+
+
+def test_decode_workspace_cache_many_streams(fa):
+    """More streams than the eager pool keeps (8 per device): the least recently
+    used buffers are dropped and remade, results unchanged."""
+    g = gen(12)
+    q, k, v = randn(g, 1, 32, 1, 128), randn(g, 1, 8, 4097, 128), randn(g, 1, 8, 4097, 128)
+    qc, kc, vc = cuda(q, k, v)
+    ref = fa.forward_decode_gqa_fp16(qc, kc, vc, True, 4096)
+    assert_close(ref, A.decode(q, k, v, True, 4096), what="decode")
+    torch.cuda.synchronize()
+    for rnd in range(2):
+        streams = [torch.cuda.Stream() for _ in range(20)]
+        outs = []
+        for s in streams:
+            with torch.cuda.stream(s):
+                outs.append(fa.forward_decode_gqa_fp16(qc, kc, vc, True, 4096))
+        torch.cuda.synchronize()
+        for o in outs:
+            assert torch.equal(o, ref)
 
 
 # ---------------------------------------------------------------- sliding-window decode

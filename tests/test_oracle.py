@@ -13,6 +13,7 @@ The reference ships no golden vectors of its own (its tests compare against
 torch on the same GPU), so these are the pins.
 """
 import os
+import math
 
 import pytest
 import torch
@@ -523,3 +524,75 @@ def test_speculative_verify_orthogonal_and_quirks():
     assert A._first_index_quirk([False, True, True]) == 1
     assert A._first_index_quirk([True]) == 0
     assert A._first_index_quirk([False, False]) == 0
+
+
+# ---- tensor-parallel helpers (same-device copies and the fp16 accumulate) ----
+
+@pytest.mark.parametrize("total,start,count", [(16, 0, 4), (16, 0, 8), (16, 5, 3), (16, 0, 16), (16, 15, 1),
+                                               (16, 7, 0), (3, 1, 2)])
+def test_scatter_gather_heads_equal_slicing(total, start, count):
+    """The reference's per-element index map (three divisions per element) is a
+    head-range slice: scatter == full[:, start:start+count]; gather writes that
+    slice and leaves every other head untouched; gather(scatter(x)) == x there."""
+    g = torch.Generator().manual_seed(total * 100 + start * 10 + count)
+    B, N, D = 2, 5, 6
+    full = torch.randn(B, total, N, D, generator=g).half()
+    local0 = torch.randn(B, count, N, D, generator=g).half()
+    loc = A.scatter_heads(full, local0, total, start, count)
+    assert torch.equal(loc, full[:, start:start + count])
+    base = torch.randn(B, total, N, D, generator=g).half()
+    got = A.gather_heads(base, local0, total, start, count)
+    ref = base.clone()
+    ref[:, start:start + count] = local0
+    assert torch.equal(got, ref)
+    assert torch.equal(A.gather_heads(torch.zeros_like(full), loc, total, start, count)[:, start:start + count],
+                       full[:, start:start + count])
+
+
+def test_scatter_gather_reference_case():
+    """test_multi_gpu.py:44-70: seed 42, B=2, H=16, N=128, D=64, counts 4 and 8
+    from head 0; scatter equals the leading heads, gather reconstructs them."""
+    torch.manual_seed(42)
+    B, H, N, D = 2, 16, 128, 64
+    full = torch.randn(B, H, N, D).half()
+    for c in (4, 8):
+        loc = A.scatter_heads(full, torch.zeros(B, c, N, D).half(), H, 0, c)
+        assert (loc.float() - full[:, :c].float()).abs().max().item() < 1e-6
+        rec = A.gather_heads(torch.zeros_like(full), loc, H, 0, c)
+        assert torch.equal(rec[:, :c], full[:, :c]) and not rec[:, c:].any()
+
+
+def test_allreduce_fp16_is_correctly_rounded_sum():
+    """fp16 + fp16 widened to fp32, added (RNE) and narrowed (RNE) equals the
+    exact sum rounded once to fp16: fp32 carries 24 >= 2*11 + 2 significand
+    bits, so the double rounding is innocuous (Figueroa, 1995).  Checked for
+    every fp16 bit pattern against a set of partners that produce ties, carries,
+    cancellation, subnormals and overflow; the exact sum is computed in fp64,
+    where the sum of two fp16 values is exact."""
+    import numpy as np
+
+    a = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    partners = np.array([0.0, -0.0, 1.0, -1.0, 2.0 ** -24, -(2.0 ** -24), 2.0 ** -14, 0.5, 3.0, 1024.5,
+                         2049.0, 65504.0, -65504.0, 16.0, 0.333, 1e-3, 7.0e4, np.inf, -np.inf], dtype=np.float64)
+    partners = partners.astype(np.float16)
+    for p in partners:
+        b = np.full_like(a, p)
+        got = A.allreduce_fp16(torch.from_numpy(a.copy()), torch.from_numpy(b)).numpy()
+        with np.errstate(over="ignore", invalid="ignore"):
+            exact = (a.astype(np.float64) + b.astype(np.float64)).astype(np.float16)
+        nan = np.isnan(exact)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint16), exact[~nan].view(np.uint16)), float(p)
+
+
+def test_allreduce_fp16_known_answers():
+    """Ties to even (2048 + 1 -> 2048, 2050 + 1 -> 2052), overflow past the
+    rounding midpoint (65504 + 16 -> inf), exact cancellation (+0), NaN."""
+    import numpy as np
+
+    d = torch.tensor([2048.0, 2050.0, 65504.0, 1.5, float("nan"), 65504.0]).half()
+    s = torch.tensor([1.0, 1.0, 16.0, -1.5, 1.0, 8.0]).half()
+    r = A.allreduce_fp16(d, s)
+    assert r[:4].tolist() == [2048.0, 2052.0, float("inf"), 0.0]
+    assert math.isnan(r[4].item()) and r[5].item() == 65504.0
+    assert not np.signbit(r[3].numpy())
