@@ -91,36 +91,34 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 __device__ __forceinline__ void store_coherent(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// gfx950 lane swaps, in place: permlane32_swap exchanges lanes 32-63 of `a`
+// with lanes 0-31 of `b`; permlane16_swap exchanges the odd 16-lane rows of
+// `a` with the even rows of `b`.  Inline asm: the compiler's two-result
+// builtins were observed to reuse one result register for both results
+// (ROCm 7.2, hipcc -O3), which silently drops the swap.
+__device__ __forceinline__ void permlane32_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ void permlane16_swap(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+// 16-byte device-coherent (sc1, write-through) store of a float4.
+__device__ __forceinline__ void store_coherent4(float* p, float4_t v) {
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Sixteen device-coherent (sc1) loads of a float4 row slice and a float scalar
-// each -- v[j] = rows[idx[j] * row_stride .. +4), s[j] = scal[idx[j]] -- issued
-// back to back and completed by one wait, i.e. one memory round trip.  The
-// compiler offers no 16-byte coherent load (a volatile access is followed by a
-// wait after every load), so the loads are inline asm; the closing wait names
-// every destination as an operand, so no use can be scheduled before it.
-__device__ __forceinline__ void load_coherent_batch16(const float* rows, int row_stride, const float* scal,
-                                                      const int (&idx)[16], float4_t (&v)[16], float (&s)[16]) {
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    asm volatile("global_load_dwordx4 %0, %1, off sc1"
-                 : "=v"(v[j]) : "v"(rows + static_cast<size_t>(idx[j]) * row_stride) : "memory");
-    asm volatile("global_load_dword %0, %1, off sc1" : "=v"(s[j]) : "v"(scal + idx[j]) : "memory");
-  }
-  asm volatile("s_waitcnt vmcnt(0)"
-               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]),
-                 "+v"(v[8]), "+v"(v[9]), "+v"(v[10]), "+v"(v[11]), "+v"(v[12]), "+v"(v[13]), "+v"(v[14]), "+v"(v[15]),
-                 "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3]), "+v"(s[4]), "+v"(s[5]), "+v"(s[6]), "+v"(s[7])
-               :: "memory");
-  // Ordered after the wait (volatile asm keeps program order); ties the rest.
-  asm volatile("" : "+v"(s[8]), "+v"(s[9]), "+v"(s[10]), "+v"(s[11]), "+v"(s[12]), "+v"(s[13]), "+v"(s[14]), "+v"(s[15])
-               :: "memory");
-}
 
 // s_waitcnt vmcnt(0): this thread's vector memory operations, stores included,
 // have completed.  (GFX9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15.)
+__device__ __forceinline__ void wait_vmem() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): every vector memory load and store done
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
 __device__ __forceinline__ void wait_vmem_stores() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0x0F70);

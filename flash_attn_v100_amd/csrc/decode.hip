@@ -43,6 +43,9 @@ constexpr int kPage = 16;             // PAGE_BLOCK_SIZE of the paged cache
 #ifndef FA_DEC_CHUNK_QUANTUM
 #define FA_DEC_CHUNK_QUANTUM 256
 #endif
+constexpr unsigned kCounterSlotsDev = 65536;  // arrival counters in the workspace
+// Polls of one ready flag before the merging split gives up (about 0.1 s).
+constexpr unsigned kMergeSpinLimit = 1u << 20;
 constexpr int kMaxChunk = 8192;                        // keys per split, upper bound
 constexpr int kChunkQuantum = FA_DEC_CHUNK_QUANTUM;    // split boundaries are multiples of this
 constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many split workgroups
@@ -59,6 +62,7 @@ constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / FA_DEC_PAGED_DIV;
 #define FA_DEC_TARGET_BLOCKS_FIXED 640
 #endif
 constexpr int kTargetBlocksFixed = FA_DEC_TARGET_BLOCKS_FIXED;
+constexpr int kFixedQuantum = 256;  // fixed-length split boundaries (kSmallGridQuantum below)
 constexpr int kMaxSplits = 128;
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
@@ -78,7 +82,10 @@ struct DecodeParams {
   const float* k_scale;        // INT8
   float* ws_o;                 // [B*H_Q, S, DP] normalised partial outputs
   float* ws_lse;               // [B*H_Q, S] log2-sum-exp of each partial
-  unsigned* counters;          // [kCounterSlots] arrivals per unit of a launch; zero between calls
+  unsigned* counters;          // [2 * kCounterSlots] arrivals, then publications, per unit; zero between calls
+  unsigned* flags;             // [kFlagWords] per-split ready flags (slot * S + split); zero between calls
+  int use_flags;               // this launch publishes through flags (units * S <= kFlagWords)
+  int early_merge;             // arrival ranks at the start, merger waits for publication
   int unit_base;               // first unit of this launch
   int B, H_Q, H_KV, N, D, G;
   int fixed_len;               // decode / INT8: number of attended keys
@@ -175,8 +182,21 @@ struct PExchange {
   static constexpr int kPad = GB < 4 ? 4 : GB;
 };
 
+// Arrival counter of a launch's unit slot.  Consecutive slots sit in
+// different 128-byte lines (32 counters apart), since atomics on one line
+// are serialised: with the splits of eight units counting on one line, 256
+// arrivals took up to 3 us; on separate lines about 1 us.
+__device__ __forceinline__ int counter_index(int slot) {
+  constexpr int kLines = static_cast<int>(kCounterSlotsDev / 32);
+  return (slot % kLines) * 32 + slot / kLines;
+}
+
 template <int DP, int GB, int MODE, bool VEC>
-__global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParams p) {
+// Three waves per SIMD (a 168-register budget): every mode's tile loop fits
+// it without spilling, and the compiler's own choice for the INT8 KV cache
+// (128 registers and a spill, for four waves) measured 14 % slower.
+__global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
+    DecodeParams p) {
   constexpr int NC = DP / 32;                 // 32-column slices of the QK^T product
   constexpr int LPR = DP / 8;                 // lanes per key row in the row layout
   constexpr int RPW = 64 / LPR;               // rows covered by one row-layout load
@@ -189,7 +209,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
 
   const int S = p.num_splits;
   const int split = blockIdx.x % S;
-  const int slot = blockIdx.x / S;      // this launch's counter slot
+  const int slot = blockIdx.x / S;  // this launch's counter slot
   const int rest = p.unit_base + slot;  // (b, h_kv, head group) unit
   const int hg = rest % p.num_hg;
   const int pair = rest / p.num_hg;
@@ -257,6 +277,16 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
     }
     return;
   }
+
+  // Splits that hold keys of this sequence (>= 1 here, since k0 < k1).
+  const int sb = min(S, (L + p.chunk - 1) / p.chunk);
+  // Early merge (small grids): the arrival rank among the unit's splits is
+  // taken now, so the atomic's round trip overlaps the key loads, and the
+  // split that arrives last merges, waiting for the others to publish.
+  // Otherwise the rank is taken once the partial is written, and the split
+  // that finishes last merges without waiting.
+  unsigned arrival = 0;
+  if (p.early_merge && sb > 1 && tid == 0) arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
 
   // Paged: the page ids of the keys [r0, r1) being walked are staged in LDS,
   // kMaxChunk keys per round (one round unless the sequence overruns its
@@ -561,46 +591,47 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
   };
 
   const int stride = kDecWaves * TK;
-  static_assert(kMaxChunk % (kDecWaves * 32) == 0, "page rounds hold whole wave iterations");
-  for (int rb = k0; rb < k1; rb += kMaxChunk) {
-  const int re = (MODE == kModePaged && k1 - rb > kMaxChunk) ? rb + kMaxChunk : k1;
-  if constexpr (MODE == kModePaged) {
-    if (rb != k0) __syncthreads();  // every wave is done with the previous round's ids
-    stage_pages(rb, re);
-  }
-  for (int t0 = rb + wave * TK; t0 < re; t0 += stride) {
-    Tile A;
-    if constexpr (MODE == kModeInt8KV) {
-      Tile8 R;
-      load_tile8(R, t0);
+  // The waves walk the keys [from, to) in strides of kDecWaves * TK.  (The
+  // tiles are locals of the loop body: kept in registers, not behind a
+  // reference, or the compiler moves the INT8 scales to scratch memory.)
+  auto walk = [&](int from, int to) {
+    for (int t0 = from + wave * TK; t0 < to; t0 += stride) {
+      Tile A;
+      if constexpr (MODE == kModeInt8KV) {
+        Tile8 R;
+        load_tile8(R, t0);
 #pragma unroll
-      for (int tt = 0; tt < T16; ++tt)
+        for (int tt = 0; tt < T16; ++tt)
 #pragma unroll
-        for (int c = 0; c < NC; ++c) A.k[tt][c] = dequant_i8x8(R.k[tt][c], R.ks[tt]);
+          for (int c = 0; c < NC; ++c) A.k[tt][c] = dequant_i8x8(R.k[tt][c], R.ks[tt]);
 #pragma unroll
-      for (int u = 0; u < UV; ++u) A.v[u] = dequant_i8x8(R.v[u], R.vs[u]);
-    } else {
-      load_tile(A, t0);
+        for (int u = 0; u < UV; ++u) A.v[u] = dequant_i8x8(R.v[u], R.vs[u]);
+      } else {
+        load_tile(A, t0);
+      }
+      compute_tile(A, t0);
     }
-    compute_tile(A, t0);
-  }
-  if constexpr (MODE != kModePaged) break;  // contiguous modes: one pass over [k0, k1)
+  };
+  if constexpr (MODE == kModePaged) {
+    static_assert(kMaxChunk % (kDecWaves * 32) == 0, "page rounds hold whole wave iterations");
+    for (int rb = k0; rb < k1; rb += kMaxChunk) {
+      const int re = k1 - rb > kMaxChunk ? rb + kMaxChunk : k1;
+      if (rb != k0) __syncthreads();  // every wave is done with the previous round's ids
+      stage_pages(rb, re);
+      walk(rb, re);
+    }
+  } else {
+    walk(k0, k1);
   }
 
   // ---- wave-level reduction: all lanes of a wave share mu, so plain sums ----
 #pragma unroll
   for (int r = 0; r < 4; ++r) lpart[r] = group_sum<16>(lpart[r]);
-#pragma unroll
-  for (int off = LPR; off < 64; off <<= 1)
-#pragma unroll
-    for (int g = 0; g < GB; ++g)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] += __shfl_xor(acc[g][j], off, 64);
 
   // ---- merge the waves through LDS ----
   __shared__ float s_m[kDecWaves][GP];
   __shared__ float s_l[kDecWaves][GP];
-  __shared__ float s_acc[kDecWaves][GB][DP];
+  __shared__ __attribute__((aligned(16))) float s_acc[kDecWaves][GB][DP];
   if (l16 == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -611,135 +642,303 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
       }
     }
   }
-  if (rg == 0) {
+  if constexpr (LPR == 16 && GB % 4 == 0) {
+    // The four row groups (lanes l, l^16, l^32, l^48) hold partial sums of
+    // the same columns.  Two lane-swap steps reduce four heads at once: the
+    // 32-lane swap adds rows (0,2) and (1,3) of a head pair, the 16-lane swap
+    // then adds rows (0,1) and (2,3) of two such pairs, leaving head 4hq + r
+    // fully reduced in row r.  Each lane then writes its 8 columns of one head.
+    const int r_row = lane >> 4;
 #pragma unroll
-    for (int g = 0; g < GB; ++g)
+    for (int hq = 0; hq < GB / 4; ++hq) {
+      float u[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s_acc[wave][g][col + j] = acc[g][j];
+      for (int j = 0; j < 8; ++j) {
+        float x0 = acc[4 * hq + 0][j], x1 = acc[4 * hq + 2][j];
+        float y0 = acc[4 * hq + 1][j], y1 = acc[4 * hq + 3][j];
+        permlane32_swap(x0, x1);
+        permlane32_swap(y0, y1);
+        float z0 = x0 + x1, z1 = y0 + y1;
+        permlane16_swap(z0, z1);
+        u[j] = z0 + z1;
+      }
+      float* dst = &s_acc[wave][4 * hq + r_row][col];
+      *reinterpret_cast<float4_t*>(dst) = float4_t{u[0], u[1], u[2], u[3]};
+      *reinterpret_cast<float4_t*>(dst + 4) = float4_t{u[4], u[5], u[6], u[7]};
+    }
+  } else {
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] += __shfl_xor(acc[g][j], off, 64);
+    if (rg == 0) {
+#pragma unroll
+      for (int g = 0; g < GB; ++g)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) s_acc[wave][g][col + j] = acc[g][j];
+    }
   }
   __syncthreads();
 
   bool bad = false;
   if constexpr (MODE == kModePaged) bad = s_bad != 0;
-  // Splits that hold keys of this sequence (>= 1 here, since k0 < k1).
-  const int sb = min(S, (L + p.chunk - 1) / p.chunk);
-
-  for (int i = tid; i < GB * DP; i += kDecThreads) {
-    const int g = i / DP, d = i % DP;
-    if (g >= g_valid || d >= D) continue;
-    float mx = s_m[0][g];
-#pragma unroll
-    for (int w = 1; w < kDecWaves; ++w) mx = fmaxf(mx, s_m[w][g]);
-    float lsum = 0.0f, a = 0.0f;
+  // One thread per (head, 4 columns): every LDS read of the wave merge is
+  // issued at once, then one 16-byte store of the split's partial.
+  constexpr int NC4 = DP / 4;
+  for (int i = tid; i < GB * NC4; i += kDecThreads) {
+    const int g = i / NC4, d4 = (i % NC4) * 4;
+    if (g >= g_valid || d4 >= D) continue;
+    float mw[kDecWaves], lw[kDecWaves];
+    float4_t aw[kDecWaves];
 #pragma unroll
     for (int w = 0; w < kDecWaves; ++w) {
-      const float e = fast_exp2(s_m[w][g] - mx);
-      lsum += s_l[w][g] * e;
-      a += s_acc[w][g][d] * e;
+      mw[w] = s_m[w][g];
+      lw[w] = s_l[w][g];
+      aw[w] = *reinterpret_cast<const float4_t*>(&s_acc[w][g][d4]);
     }
-    float outv = a / lsum;
+    float mx = mw[0];
+#pragma unroll
+    for (int w = 1; w < kDecWaves; ++w) mx = fmaxf(mx, mw[w]);
+    float lsum = 0.0f;
+    float4_t a = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) {
+      const float e = fast_exp2(mw[w] - mx);
+      lsum += lw[w] * e;
+      a += aw[w] * e;
+    }
+    float4_t outv = a / lsum;
     float lse = mx + __log2f(lsum);
-    if (bad) outv = lse = __builtin_nanf("");
+    if (bad) {
+      outv = float4_t{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")};
+      lse = __builtin_nanf("");
+    }
     const int h = hkv * G + g_base + g;
     const size_t bh = static_cast<size_t>(b) * p.H_Q + h;
     if (sb == 1) {
-      p.o[bh * D + d] = static_cast<half_t>(outv);
+      half_t* op = p.o + bh * D + d4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (d4 + j < D) op[j] = static_cast<half_t>(outv[j]);
     } else {
       const size_t e = bh * S + split;
-      store_coherent(&p.ws_o[e * DP + d], outv);
-      if (d == 0) store_coherent(&p.ws_lse[e], lse);
+      store_coherent4(&p.ws_o[e * DP + d4], outv);
+      if (d4 == 0) store_coherent(&p.ws_lse[e], lse);
     }
   }
   if (sb == 1) return;
 
-  // ---- the last split of this (b, h_kv, head group) to finish merges all partials ----
-  // Partials travel through device-coherent (L2-bypassing, sc1) stores and loads,
-  // so no whole-L2 writeback/invalidate fence is needed: each thread waits for its
-  // stores to complete, the barrier orders that before thread 0's counter atomic,
-  // and the last arrival reads the partials with coherent loads.
-  __shared__ int s_last;
+  // ---- publish this split's partial; the last-arriving split merges ----
+  // Partials travel through device-coherent (L2-bypassing, sc1) stores and
+  // loads, so no whole-L2 writeback/invalidate fence is needed.  Once all of
+  // a split's partial stores are complete it publishes them: with ready
+  // flags (launches of at most kFlagWords unit splits) it sets its own flag,
+  // otherwise it bumps the unit's publication counter.  The split with the
+  // last arrival rank waits until every split of the unit has published, then
+  // merges.  That wait always ends: each split that took an arrival rank
+  // before the merger is already running and needs nothing from anyone.  It
+  // is bounded all the same; past the bound the merger writes NaN.
+  __shared__ int s_last, s_timeout;
   wait_vmem_stores();
   __syncthreads();
+  unsigned* published = &p.counters[kCounterSlotsDev + counter_index(slot)];
+  unsigned* flags = p.flags + static_cast<size_t>(slot) * S;
   if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.counters[slot], 1u);
-    s_last = (prev == static_cast<unsigned>(sb - 1));
+    if (!p.early_merge) arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
+    else if (p.use_flags) __hip_atomic_store(&flags[split], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else __hip_atomic_fetch_add(published, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (arrival == static_cast<unsigned>(sb - 1));
+    s_timeout = 0;
   }
   __syncthreads();
   if (!s_last) return;
+  // Every split of the unit has taken its arrival rank: the counter can go
+  // back to zero for the next call on this workspace.
+  if (tid == 0) __hip_atomic_store(&p.counters[counter_index(slot)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  // Merge the sb partials of each head in one batch of coherent loads: thread
-  // (column group c, phase ph) reads the lse and 4 output columns of splits
-  // ph, ph + NPH, ... together, keeps its own running max, and the phases
-  // meet in LDS with a rescale -- one memory round trip for the whole merge.
+  // ---- merge ----
+  // Thread (column group c, phase ph) merges 4 output columns over the splits
+  // ph, ph + NPH, ... .  When they fit one batch (sb <= NB * NPH) the loads
+  // go in two rounds, in the same registers: first the splits already
+  // published when the merger gets here (most of them, read while the
+  // stragglers still run), then, once every split has published, the rest.
+  // The combine runs after both, in split order, so the result does not
+  // depend on which round a split fell in.  Larger sb: batches after all
+  // splits have published.  Partials are read with device-coherent (sc1)
+  // buffer loads.
   constexpr int NP = GB * DP / 4;                                  // float4 columns
   constexpr int NPH = NP >= kDecThreads ? 1 : kDecThreads / NP;    // split phases
-  constexpr int NB = 16;                                           // splits per batch (load_coherent_batch16)
+  constexpr int NB = 16;                                           // splits per load batch
+  constexpr int NCOL = (NP + kDecThreads - 1) / kDecThreads;       // columns per thread
+  __shared__ unsigned long long s_ready[2];  // splits loaded in the first round
   __shared__ float4_t s_num[NPH][NPH > 1 ? NP : 1];
   __shared__ float s_mx[NPH][NPH > 1 ? NP : 1];
   __shared__ float s_den[NPH][NPH > 1 ? NP : 1];
+  const size_t unit_bh = static_cast<size_t>(b) * p.H_Q + hkv * G + g_base;
+  const __amdgpu_buffer_rsrc_t ws_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_o + unit_bh * S * DP, 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t lse_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(p.ws_lse + unit_bh * S, 0, 0x7fffffff, 0x00020000);
   struct Part {
     float4_t num;
     float mx, den;
   };
-  auto column_merge = [&](int c, int ph) -> Part {
-    Part r = {float4_t{0.0f, 0.0f, 0.0f, 0.0f}, -INFINITY, 0.0f};
+  auto column_ok = [&](int c) { return c < NP && c / (DP / 4) < g_valid && (c % (DP / 4)) * 4 < D; };
+  // loads split sp of column c into (v, l)
+  auto load_split = [&](int c, int sp, float4_t& v, float& l) {
     const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
-    if (g >= g_valid || d4 >= D) return r;
-    const size_t bh = static_cast<size_t>(b) * p.H_Q + hkv * G + g_base + g;
-    const float* po = p.ws_o + bh * S * DP + d4;
-    const float* pl = p.ws_lse + bh * S;
-    for (int sp = ph; sp < sb; sp += NB * NPH) {
-      float lv[NB];
-      float4_t v[NB];
-      int qs[NB];
+    v = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                         ws_rsrc, ((g * S + sp) * DP + d4) * static_cast<int>(sizeof(float)), 0, 16));
+    l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                      lse_rsrc, (g * S + sp) * static_cast<int>(sizeof(float)), 0, 16));
+  };
+  // online combine of one batch in split order
+  auto combine = [&](Part& r, const float4_t (&v)[NB], const float (&lv)[NB]) {
+    float m = r.mx;
 #pragma unroll
-      for (int j = 0; j < NB; ++j) qs[j] = min(sp + j * NPH, sb - 1);  // in-range address, masked below
-      load_coherent_batch16(po, DP, pl, qs, v, lv);
+    for (int j = 0; j < NB; ++j) m = fmaxf(m, lv[j]);
+    const float a = fast_exp2(r.mx - m);
+    r.num *= a;
+    r.den *= a;
 #pragma unroll
-      for (int j = 0; j < NB; ++j)
-        if (sp + j * NPH >= sb) {
-          lv[j] = -INFINITY;
-          v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NB; ++j) {
+      const float w = fast_exp2(lv[j] - m);
+      r.den += w;
+      r.num += w * v[j];
+    }
+    r.mx = m;
+  };
+  // Waits until every split has published (flags: wave 0, a lane per split,
+  // skipping those seen in the first round; counter: one thread).
+  auto wait_all = [&](unsigned long long seen0, unsigned long long seen1) {
+    if (p.use_flags) {
+      if (wave == 0) {
+        for (int h = 0; h < 2; ++h) {
+          const int sp = lane + 64 * h;
+          if (sp < sb && !(((h ? seen1 : seen0) >> lane) & 1ull)) {
+            unsigned spins = 0;
+            while (__hip_atomic_load(&flags[sp], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+              if (++spins > kMergeSpinLimit) {
+                s_timeout = 1;
+                break;
+              }
+              __builtin_amdgcn_s_sleep(1);
+            }
+          }
         }
-      float m = r.mx;
-#pragma unroll
-      for (int j = 0; j < NB; ++j) m = fmaxf(m, lv[j]);
-      const float a = fast_exp2(r.mx - m);
-      r.num *= a;
-      r.den *= a;
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const float w = fast_exp2(lv[j] - m);
-        r.den += w;
-        r.num += w * v[j];
       }
-      r.mx = m;
-    }
-    return r;
-  };
-  auto store_out = [&](int c, float4_t o) {
-    const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
-    if (g >= g_valid || d4 >= D) return;
-    half_t* op = p.o + (static_cast<size_t>(b) * p.H_Q + hkv * G + g_base + g) * D + d4;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (d4 + j < D) op[j] = static_cast<half_t>(o[j]);
-  };
-  if constexpr (NPH == 1) {
-    for (int c = tid; c < NP; c += kDecThreads) {
-      const Part r = column_merge(c, 0);
-      store_out(c, r.num / r.den);
-    }
-  } else {
-    const int c = tid % NP, ph = tid / NP;
-    if (ph < NPH) {
-      const Part r = column_merge(c, ph);
-      s_num[ph][c] = r.num;
-      s_mx[ph][c] = r.mx;
-      s_den[ph][c] = r.den;
+    } else if (tid == 0) {
+      unsigned spins = 0;
+      while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < static_cast<unsigned>(sb)) {
+        if (++spins > kMergeSpinLimit) {
+          s_timeout = 1;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
     }
     __syncthreads();
-    if (tid < NP) {
+    // Every split has published: leave the flags (or the publication
+    // counter) at zero for the next call on this workspace now, so the stores
+    // overlap the merge instead of delaying the kernel's end.
+    if (p.use_flags) {
+      if (tid < sb) __hip_atomic_store(&flags[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (tid == 0) {
+      __hip_atomic_store(published, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+  const int c_mine = NPH > 1 ? tid % NP : tid;
+  const int ph = NPH > 1 ? tid / NP : 0;
+  Part parts[NCOL];
+#pragma unroll
+  for (int q = 0; q < NCOL; ++q) parts[q] = Part{float4_t{0.0f, 0.0f, 0.0f, 0.0f}, -INFINITY, 0.0f};
+  if (p.early_merge && NCOL == 1 && sb <= NB * NPH) {
+    // first round: the splits published so far
+    unsigned long long r0 = 0, r1 = 0;
+    if (p.use_flags && wave == 0) {
+      const bool f0 = lane < sb && __hip_atomic_load(&flags[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+      const bool f1 =
+          lane + 64 < sb && __hip_atomic_load(&flags[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+      r0 = __builtin_amdgcn_ballot_w64(f0);
+      r1 = __builtin_amdgcn_ballot_w64(f1);
+      if (lane == 0) {
+        s_ready[0] = r0;
+        s_ready[1] = r1;
+      }
+    } else if (!p.use_flags && tid == 0) {
+      s_ready[0] = s_ready[1] = 0ull;
+    }
+    __syncthreads();
+    const unsigned long long m0 = s_ready[0], m1 = s_ready[1];
+    auto ready = [&](int sp) { return ((sp < 64 ? m0 : m1) >> (sp & 63)) & 1ull; };
+    const bool active = ph < NPH && ph < sb && column_ok(c_mine);
+    float4_t v[NB];
+    float lv[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      lv[j] = -INFINITY;
+      const int sp = ph + j * NPH;
+      if (active && sp < sb && ready(sp)) load_split(c_mine, sp, v[j], lv[j]);
+    }
+    // second round: the rest, once published.  The first round's loads are
+    // completed first (they had the wait to land), so the second round's
+    // loads into the same registers need no wait of their own.
+    wait_all(m0, m1);
+    wait_vmem();
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const int sp = ph + j * NPH;
+      if (active && sp < sb && !ready(sp)) load_split(c_mine, sp, v[j], lv[j]);
+    }
+    if (active) combine(parts[0], v, lv);
+  } else {
+    if (p.early_merge) wait_all(0ull, 0ull);
+    if (ph < NPH) {
+#pragma unroll
+      for (int q = 0; q < NCOL; ++q) {
+        const int c = c_mine + q * kDecThreads;
+        if (!column_ok(c)) continue;
+        for (int k0 = ph; k0 < sb; k0 += NB * NPH) {
+          float4_t v[NB];
+          float lv[NB];
+#pragma unroll
+          for (int j = 0; j < NB; ++j) {
+            v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+            lv[j] = -INFINITY;
+            const int sp = k0 + j * NPH;
+            if (sp < sb) load_split(c, sp, v[j], lv[j]);
+          }
+          combine(parts[q], v, lv);
+        }
+      }
+    }
+  }
+  const bool timed_out = s_timeout != 0;
+
+  auto store_out = [&](int c, float4_t o) {
+    const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
+    half_t* op = p.o + (unit_bh + g) * D + d4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (d4 + j < D) op[j] = static_cast<half_t>(timed_out ? __builtin_nanf("") : o[j]);
+  };
+  if constexpr (NPH == 1) {
+#pragma unroll
+    for (int q = 0; q < NCOL; ++q) {
+      const int c = c_mine + q * kDecThreads;
+      if (column_ok(c)) store_out(c, parts[q].num / parts[q].den);
+    }
+  } else {
+    if (ph < NPH) {
+      s_num[ph][c_mine] = parts[0].num;
+      s_mx[ph][c_mine] = parts[0].mx;
+      s_den[ph][c_mine] = parts[0].den;
+    }
+    __syncthreads();
+    if (tid < NP && column_ok(tid)) {
       float m = s_mx[0][tid];
 #pragma unroll
       for (int q = 1; q < NPH; ++q) m = fmaxf(m, s_mx[q][tid]);
@@ -754,8 +953,6 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(DecodeParam
       store_out(tid, num / den);
     }
   }
-  // Leave the counter at zero for the next call on this workspace.
-  if (tid == 0) atomicExch(&p.counters[slot], 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -774,7 +971,7 @@ static int pick_gb(int g) { return g <= 1 ? 1 : (g <= 2 ? 2 : (g <= 4 ? 4 : (g <
 // a split of its own (e.g. 4097 keys in 256-key splits: 16 splits, not 17 --
 // one workgroup and one merge round trip less).
 static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int target_blocks,
-                            bool absorb_tail = false) {
+                            bool absorb_tail = false, int quantum = kChunkQuantum) {
   DecodePlan pl;
   const int G = H_Q / H_KV;
   pl.dp = pick_dp(D);
@@ -782,11 +979,11 @@ static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int ta
   pl.num_hg = ceil_div(G, pl.gb);
   const long long units = static_cast<long long>(B) * H_KV * pl.num_hg;
   long long want = (static_cast<long long>(max_len > 0 ? max_len : 1) * units + target_blocks - 1) / target_blocks;
-  long long chunk = ((want + kChunkQuantum - 1) / kChunkQuantum) * kChunkQuantum;
+  long long chunk = ((want + quantum - 1) / quantum) * quantum;
   // at most kMaxSplits splits per sequence
   const long long min_chunk = (static_cast<long long>(max_len) + kMaxSplits - 1) / kMaxSplits;
-  if (chunk < min_chunk) chunk = ((min_chunk + kChunkQuantum - 1) / kChunkQuantum) * kChunkQuantum;
-  if (chunk < kChunkQuantum) chunk = kChunkQuantum;
+  if (chunk < min_chunk) chunk = ((min_chunk + quantum - 1) / quantum) * quantum;
+  if (chunk < quantum) chunk = quantum;
   if (chunk > kMaxChunk) chunk = kMaxChunk;
   pl.chunk = static_cast<int>(chunk);
   pl.splits = max_len > 0 ? ceil_div(max_len, chunk) : 1;
@@ -799,25 +996,32 @@ static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int ta
 
 static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-// Workspace layout: [counters: kCounterSlots x u32][lse: B*H_Q*S f32][partials: B*H_Q*S*DP f32],
+// Workspace layout: [counters: 2 x kCounterSlots u32][flags: kFlagWords u32][lse: B*H_Q*S f32]
+// [partials: B*H_Q*S*DP f32],
 // each region 256-byte aligned.  Needed only when a sequence can span several
-// splits.  The counter region has the same size and place for every call, so
-// one workspace can serve calls of any shape: no call's partials ever land on
-// another call's counters.  A launch covers at most kCounterSlots units; larger
+// splits.  The counter and flag regions have the same size and place for every
+// call, so one workspace can serve calls of any shape: no call's partials ever
+// land on another call's counters or flags.  A launch covers at most kCounterSlots units; larger
 // problems are issued as several launches over unit ranges.
-constexpr size_t kCounterSlots = 65536;
+constexpr size_t kCounterSlots = kCounterSlotsDev;
+// The counter region holds kCounterSlots arrival counters, then as many
+// publication counters.
+constexpr size_t kCounterWords = 2 * kCounterSlots;
+// Per-split ready flags, used by launches whose units x splits fit.
+constexpr size_t kFlagWords = 65536;
 
 struct WorkspaceLayout {
-  size_t counters, lse, o, total;
+  size_t counters, flags, lse, o, total;
 };
 
 static WorkspaceLayout plan_layout(const DecodePlan& pl, int B, int H_Q, int H_KV) {
   (void)H_KV;
-  WorkspaceLayout w = {0, 0, 0, 0};
+  WorkspaceLayout w = {0, 0, 0, 0, 0};
   if (pl.splits <= 1) return w;
   const size_t entries = static_cast<size_t>(B) * H_Q * pl.splits;
   w.counters = 0;
-  w.lse = align256(kCounterSlots * sizeof(unsigned));
+  w.flags = align256(kCounterWords * sizeof(unsigned));
+  w.lse = w.flags + align256(kFlagWords * sizeof(unsigned));
   w.o = w.lse + align256(entries * sizeof(float));
   w.total = w.o + entries * pl.dp * sizeof(float);
   return w;
@@ -866,12 +1070,30 @@ static int target_blocks() {
   return MODE == kModePaged ? kTargetBlocksPaged : (MODE == kModeCB ? kTargetBlocks : kTargetBlocksFixed);
 }
 
+// The split plan of a call.  Fixed-length calls split at multiples of
+// kFixedQuantum keys; when that leaves CUs idle (fewer split workgroups than
+// kSmallGridBlocks) they split at kSmallGridQuantum instead: one 32-key tile
+// per wave, every load of the call issued at once (config 2: 16 -> 32 splits
+// per head, 128 -> 256 workgroups).
+constexpr int kSmallGridQuantum = kDecWaves * 32;
+constexpr long long kSmallGridBlocks = 256;
+
+template <int MODE>
+static DecodePlan plan_for(int B, int H_Q, int H_KV, int max_len, int D) {
+  constexpr bool kFixed = MODE == kModeDecode || MODE == kModeInt8 || MODE == kModeInt8KV;
+  if (!kFixed) return make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), false, kChunkQuantum);
+  DecodePlan pl = make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), true, kFixedQuantum);
+  const long long blocks = static_cast<long long>(B) * H_KV * pl.num_hg * pl.splits;
+  if (blocks < kSmallGridBlocks) pl = make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), true, kSmallGridQuantum);
+  return pl;
+}
+
 // max_len: keys of the longest sequence the call attends (fixed-length modes:
 // exactly the attended count, which is at most N).
 template <int MODE>
 static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, size_t ws_bytes, void* stream) {
   constexpr bool kFixed = MODE == kModeDecode || MODE == kModeInt8 || MODE == kModeInt8KV;
-  const DecodePlan pl = make_plan(p.B, p.H_Q, p.H_KV, max_len, p.D, target_blocks<MODE>(), kFixed);
+  const DecodePlan pl = plan_for<MODE>(p.B, p.H_Q, p.H_KV, max_len, p.D);
   p.absorb_tail = kFixed ? 1 : 0;
   const WorkspaceLayout wl = plan_layout(pl, p.B, p.H_Q, p.H_KV);
   const size_t need = wl.total;
@@ -890,6 +1112,7 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   if (need > 0) {
     char* base = static_cast<char*>(ws);
     p.counters = reinterpret_cast<unsigned*>(base + wl.counters);
+    p.flags = reinterpret_cast<unsigned*>(base + wl.flags);
     p.ws_lse = reinterpret_cast<float*>(base + wl.lse);
     p.ws_o = reinterpret_cast<float*>(base + wl.o);
   }
@@ -901,6 +1124,8 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   for (long long u0 = 0; u0 < units; u0 += static_cast<long long>(kCounterSlots)) {
     const long long nu = units - u0 < static_cast<long long>(kCounterSlots) ? units - u0 : kCounterSlots;
     p.unit_base = static_cast<int>(u0);
+    p.use_flags = nu * pl.splits <= static_cast<long long>(kFlagWords) ? 1 : 0;
+    p.early_merge = nu * pl.splits <= kSmallGridBlocks ? 1 : 0;
     dispatch<MODE>(pl, vec, p, static_cast<int>(nu * pl.splits), st);
     const int rc = check_launch(fn);
     if (rc != FA_OK) return rc;
@@ -914,8 +1139,12 @@ using namespace fa;
 
 extern "C" size_t fa_decode_workspace_size(int B, int H_Q, int H_KV, int max_len, int D) {
   if (B <= 0 || H_Q <= 0 || H_KV <= 0 || D <= 0 || D > 256 || H_Q % H_KV != 0) return 0;
-  // The contiguous plan has the most splits, so its size covers every mode.
-  return plan_layout(make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocks), B, H_Q, H_KV).total;
+  // Large enough for the plan of every mode: the per-sequence plan (most
+  // workgroups) and the fixed-length plan (finest split quantum).
+  const size_t a = plan_layout(make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocks), B, H_Q, H_KV).total;
+  const size_t b = plan_layout(make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocksFixed, true, kSmallGridQuantum), B,
+                               H_Q, H_KV).total;
+  return a > b ? a : b;
 }
 
 extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void* o, int B, int H_Q,
