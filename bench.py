@@ -51,9 +51,6 @@ def parse():
     ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b,8,9")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
-                    help="instead of benchmarking, copy an MB-sized fp16 buffer 20 times (a kernel of "
-                         "known HBM traffic, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     return ap.parse_args()
 
 
@@ -467,16 +464,6 @@ def main():
 
     import torch
 
-    if args.copy_calibration:
-        n = args.copy_calibration * (1 << 20) // 2
-        src = torch.ones(n, dtype=torch.float16, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(20):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes_per_copy": 2 * n, "copies": 20}))
-        return
-
     import flash_attn_v100 as fa
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -485,25 +472,39 @@ def main():
     if args.only_headline:
         want = ["2"]
     results, samples = {}, {}
+    # Timed calls per config: config 2 takes --steps/--warmup as given; the
+    # others scale them by their own base counts (a few hundred microseconds
+    # to a few milliseconds per call), and every config reports what it ran.
+    base = {"1": (500, 50), "2": (200, 20), "3": (30, 5), "4": (30, 5), "5a": (50, 10), "5b": (100, 10),
+            "6a": (100, 10), "6b": (100, 10), "7": (20, 3), "7b": (5, 1), "8": (100, 10), "9": (50, 5)}
+
+    def counts(c):
+        st, wu = base[c]
+        if c == "2":
+            return args.steps, args.warmup
+        return max(1, round(st * args.steps / 200)), max(1, round(wu * args.warmup / 20))
+
     runners = {
-        "1": lambda: cfg1_prefill(fa, torch, 500, 50),
-        "2": lambda: cfg2_decode(fa, torch, args.steps, args.warmup),
-        "3": lambda: cfg3_cb(fa, torch, 30, 5),
-        "4": lambda: cfg4_paged(fa, torch, 30, 5),
-        "5a": lambda: cfg5a_varlen(fa, torch, 50, 10),
-        "5b": lambda: cfg5b_int8(fa, torch, 100, 10),
-        "6a": lambda: cfg6a_int8_kv_cache(fa, torch, 100, 10),
-        "6b": lambda: cfg6b_sliding_window(fa, torch, 100, 10),
-        "7": lambda: cfg7_backward(fa, torch, 20, 3, "fp16"),
-        "7b": lambda: cfg7_backward(fa, torch, 5, 1, "fp32"),
-        "8": lambda: cfg8_token_eviction(fa, torch, 100, 10),
-        "9": lambda: cfg9_speculative_verify(fa, torch, 50, 5),
+        "1": lambda st, wu: cfg1_prefill(fa, torch, st, wu),
+        "2": lambda st, wu: cfg2_decode(fa, torch, st, wu),
+        "3": lambda st, wu: cfg3_cb(fa, torch, st, wu),
+        "4": lambda st, wu: cfg4_paged(fa, torch, st, wu),
+        "5a": lambda st, wu: cfg5a_varlen(fa, torch, st, wu),
+        "5b": lambda st, wu: cfg5b_int8(fa, torch, st, wu),
+        "6a": lambda st, wu: cfg6a_int8_kv_cache(fa, torch, st, wu),
+        "6b": lambda st, wu: cfg6b_sliding_window(fa, torch, st, wu),
+        "7": lambda st, wu: cfg7_backward(fa, torch, st, wu, "fp16"),
+        "7b": lambda st, wu: cfg7_backward(fa, torch, st, wu, "fp32"),
+        "8": lambda st, wu: cfg8_token_eviction(fa, torch, st, wu),
+        "9": lambda st, wu: cfg9_speculative_verify(fa, torch, st, wu),
     }
     for c in ["1", "2", "3", "4", "5a", "5b", "6a", "6b", "7", "7b", "8", "9"]:
         if c not in want:
             continue
         log(f"config {c} ...")
-        r, s = runners[c]()
+        st, wu = counts(c)
+        r, s = runners[c](st, wu)
+        r["steps"], r["warmup"] = st, wu
         results[c], samples[c] = r, s
         log(f"config {c}: " + json.dumps({k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}))
         if c in ("3", "4"):
