@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "capi_internal.h"
 #include "common.h"
@@ -1165,6 +1166,79 @@ extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void*
   p.B = B; p.H_Q = H_Q; p.H_KV = H_KV; p.N = N; p.D = D;
   p.fixed_len = causal ? cache_len + 1 : N;
   return run_decode<kModeDecode>(fn, p, p.fixed_len, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: the split workspace lives in a static device array.
+//
+// `scratch` is one array per GPU (each device that loads this library holds
+// its own copy until the process ends).  Host code never uses its name as an
+// address: the device address comes from hipGetSymbolAddress, once per device
+// with that device current, and only that pointer is passed to kernels or
+// memory calls.  The regions the kernels expect at zero (arrival and
+// publication counters, ready flags) start at zero (static storage, and a
+// synchronous clear at set-up when the first call is not being captured),
+// and every call leaves them at zero.  Calls that overlap on one GPU share
+// the array and race.
+constexpr size_t kStaticScratchBytes = 16u << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+// Device address of this device's `scratch`, resolved on the first call.
+int static_scratch(const char* fn, void* stream, void** out) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(FA_ERR_HIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(FA_ERR_UNSUPPORTED, "%s: device %d beyond %d", fn, dev, kMaxScratchDevices);
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&]() {
+    void* ptr = nullptr;
+    slot.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (slot.err != hipSuccess) return;
+    slot.ptr = ptr;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap) == hipSuccess &&
+        cap == hipStreamCaptureStatusNone) {
+      const size_t zero_bytes = kCounterWords * sizeof(unsigned) + kFlagWords * sizeof(unsigned) + 512;
+      slot.err = hipMemset(ptr, 0, zero_bytes);
+    }
+  });
+  if (slot.err != hipSuccess)
+    return set_error(FA_ERR_HIP, "%s: static scratch set-up: %s", fn, hipGetErrorString(slot.err));
+  *out = slot.ptr;
+  return FA_OK;
+}
+}  // namespace
+
+extern "C" int fa_decode_fp16_noalloc(const void* q, const void* k, const void* v, void* o, int B, int H_Q,
+                                      int H_KV, int N, int D, int causal, int cache_len, void* stream) {
+  const char* fn = "fa_decode_fp16_noalloc";
+  int rc = check_common(fn, B, H_Q, H_KV, D);
+  if (rc != FA_OK) return rc;
+  if (N <= 0) return set_error(FA_ERR_INVALID_ARG, "%s: N must be positive", fn);
+  if (cache_len < 0 || cache_len >= N)
+    return set_error(FA_ERR_INVALID_ARG, "%s: cache_len=%d must lie in [0, N=%d)", fn, cache_len, N);
+  const int attended = causal ? cache_len + 1 : N;
+  const size_t need = plan_layout(plan_for<kModeDecode>(B, H_Q, H_KV, attended, D), B, H_Q, H_KV).total;
+  if (need > kStaticScratchBytes)
+    return set_error(FA_ERR_UNSUPPORTED,
+                     "%s: this call needs a %zu-byte split workspace; the static scratch holds %zu bytes "
+                     "(use fa_decode_fp16 with a caller workspace)", fn, need, kStaticScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = static_scratch(fn, stream, &ws);
+    if (rc != FA_OK) return rc;
+  }
+  return fa_decode_fp16(q, k, v, o, B, H_Q, H_KV, N, D, causal, cache_len, ws, need, stream);
 }
 
 extern "C" int fa_decode_sliding_window_gqa(const void* q, const void* k, const void* v, void* o, int B,

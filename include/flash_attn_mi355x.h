@@ -149,6 +149,22 @@ int fa_decode_fp16(const void* q, const void* k, const void* v, void* o,
                    void* stream);
 
 /*
+ * fa_decode_fp16 without a caller workspace, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, hosts that forbid
+ * device allocation).  It has no counterpart in the reference.  Same
+ * arguments and results as fa_decode_fp16; the split workspace is a static
+ * 16 MiB device array of the library, one per GPU, held until the process
+ * ends, so the call allocates nothing.  A call whose workspace would exceed
+ * it returns FA_ERR_UNSUPPORTED (fa_decode_workspace_size gives the need of
+ * the widest plan; small-batch decode such as B=1, 32:8 heads, 4097 keys,
+ * D=128 needs about 1.3 MB).  Calls that may overlap on one GPU share that
+ * array and race: issue them in order (one stream, or joined streams).
+ */
+int fa_decode_fp16_noalloc(const void* q, const void* k, const void* v, void* o,
+                           int B, int H_Q, int H_KV, int N, int D, int causal,
+                           int cache_len, void* stream);
+
+/*
  * GQA decode against an INT8 KV cache with per-token fp16 scales.
  *   k_int8/v_int8 int8 [B, H_KV, N, D]; k_scale/v_scale fp16 [B, H_KV, N].
  *   Element (t, d) is used as half(code * scale[t]); keys k <= cache_len are

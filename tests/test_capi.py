@@ -66,6 +66,17 @@ def _vp(x=0):
     return ctypes.c_void_p(x)
 
 
+def test_noalloc_decode_refuses_calls_beyond_its_static_scratch(lib):
+    """fa_decode_fp16_noalloc checks the plan's workspace against its 16 MiB
+    static array before touching any pointer or the GPU."""
+    null = _vp()
+    # B=64, 64:1 heads, 65536 keys, D=256: 8 splits x 4096 query rows of fp32 partials (33.5 MB)
+    rc = lib.fa_decode_fp16_noalloc(null, null, null, null, 64, 64, 1, 65536, 256, 1, 65535, null)
+    assert rc == FA_ERR_UNSUPPORTED and b"static scratch" in lib.fa_last_error()
+    rc = lib.fa_decode_fp16_noalloc(null, null, null, null, 1, 6, 4, 10, 64, 1, 3, null)
+    assert rc == FA_ERR_INVALID_ARG
+
+
 def test_argument_errors_are_reported_without_a_gpu(lib):
     null = _vp()
     # decode: cache_len out of range
