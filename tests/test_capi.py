@@ -213,3 +213,149 @@ def test_capi_training_on_gpu(lib):
     ref = A.backward(do, q, k, v, o.cpu(), lse.cpu(), True)
     for name, a, r in zip(("dq", "dk", "dv"), (dq, dk, dv), ref):
         assert_close(a, r, atol=3e-2, rtol=3e-2, what=f"capi backward {name}")
+
+
+def _st():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.gpu
+def test_capi_every_decode_entry_point_shares_one_workspace(lib):
+    """Continuous batching, paged, INT8, INT8 KV cache and sliding-window decode
+    through ctypes, all on ONE caller-owned workspace (sized for the largest of
+    them, zero-filled once), interleaved with the contiguous decode: each
+    matches the oracle and the workspace's counters end at zero."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    g = torch.Generator().manual_seed(31)
+    B, HQ, HKV, D = 3, 16, 4, 128
+    nbytes = max(lib.fa_decode_workspace_size(B, HQ, HKV, n, D) for n in (2000, 4096))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    wsp, wsn = _p(ws), ctypes.c_size_t(nbytes)
+    # continuous batching
+    N = 2000
+    q, k, v = randn(g, B, HQ, 1, D), randn(g, B, HKV, N, D), randn(g, B, HKV, N, D)
+    cl = torch.tensor([1999, 5, 1000], dtype=torch.int32)
+    qc, kc, vc, clc = q.cuda(), k.cuda(), v.cuda(), cl.cuda()
+    o = torch.empty_like(qc)
+    rc = lib.fa_continuous_batching_fp16(_p(qc), _p(kc), _p(vc), _p(o), _p(clc), B, HQ, HKV, N, D, 1, wsp, wsn, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert_close(o, A.continuous_batching(q, k, v, cl, True), what="capi continuous batching")
+    # contiguous decode on the same workspace
+    o = torch.empty_like(qc)
+    rc = lib.fa_decode_fp16(_p(qc), _p(kc), _p(vc), _p(o), B, HQ, HKV, N, D, 1, 1500, wsp, wsn, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert_close(o, A.decode(q, k, v, True, 1500), what="capi decode")
+    # paged: 16-token pages, a permuted table, row stride 256
+    P, MNB = 300, 256
+    kp, vp = randn(g, P, HKV, 16, D), randn(g, P, HKV, 16, D)
+    bt = torch.randint(0, P, (B, MNB), generator=g, dtype=torch.int32)
+    sl = torch.tensor([4096, 17, 700], dtype=torch.int32)
+    kpc, vpc, btc, slc = kp.cuda(), vp.cuda(), bt.cuda(), sl.cuda()
+    o = torch.empty_like(qc)
+    rc = lib.fa_paged_decode_gqa_fp16(_p(qc), _p(kpc), _p(vpc), _p(o), _p(btc), ctypes.c_int64(bt.numel()), _p(slc),
+                                      B, HQ, HKV, D, P, MNB, wsp, wsn, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert_close(o, A.paged_decode(q, kp, vp, bt, sl, MNB), what="capi paged")
+    # INT8 decode (per-head absmax/127 scales)
+    qs = (q.float().abs().amax(-1).squeeze(-1) / 127).contiguous()
+    ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(B, HKV, N).contiguous()
+    qsc, ksc = qs.cuda(), ks.cuda()
+    o = torch.empty_like(qc)
+    rc = lib.fa_decode_int8_gqa(_p(qc), _p(kc), _p(vc), _p(o), _p(qsc), _p(ksc), B, HQ, HKV, N, D, 1999,
+                                wsp, wsn, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    ref = A.decode_int8(q, k, v, qs, ks, 1999)
+    assert_close(o, ref, what="capi int8")
+    # INT8 KV cache (per-token fp16 scales)
+    def quant(x):
+        s = (x.float().abs().amax(-1, keepdim=True) / 127.0).clamp(min=1e-8)
+        return (x.float() / s).round().clamp(-128, 127).to(torch.int8), s.squeeze(-1).half()
+    k8, k8s = quant(k)
+    v8, v8s = quant(v)
+    k8c, v8c, k8sc, v8sc = k8.cuda(), v8.cuda(), k8s.cuda(), v8s.cuda()
+    o = torch.empty_like(qc)
+    rc = lib.fa_decode_int8_kv_cache_gqa(_p(qc), _p(k8c), _p(v8c), _p(k8sc), _p(v8sc), _p(o), B, HQ, HKV, N, D,
+                                         1999, wsp, wsn, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert_close(o, A.decode_int8_kv_cache(q, k8, v8, k8s, v8s, 1999), what="capi int8 kv cache")
+    # sliding window + sink
+    o = torch.empty_like(qc)
+    rc = lib.fa_decode_sliding_window_gqa(_p(qc), _p(kc), _p(vc), _p(o), B, HQ, HKV, N, D, 1800, 512, 16,
+                                          wsp, wsn, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert_close(o, A.decode_sliding_window(q, k, v, 1800, 512, 16), what="capi sliding window")
+    # the arrival/publication counters and ready flags are back at zero
+    torch.cuda.synchronize()
+    assert int(ws[: (2 * 65536 + 65536) * 4].cpu().sum()) == 0
+
+
+@pytest.mark.gpu
+def test_capi_varlen_token_ops_and_tp_helpers(lib):
+    """fa_varlen_prefill_fp16, fa_token_eviction, fa_speculative_verify and the
+    tensor-parallel copies / accumulate through ctypes."""
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    g = torch.Generator().manual_seed(32)
+    # varlen prefill: 3 sequences, one empty
+    lens = [130, 0, 77]
+    cu = torch.tensor([0, 130, 130, 207], dtype=torch.int32)
+    H, D = 4, 64
+    q, k, v = (randn(g, 207, H, D) for _ in range(3))
+    qc, kc, vc, cuc = q.cuda(), k.cuda(), v.cuda(), cu.cuda()
+    o = torch.empty_like(qc)
+    row_limit = A.varlen_row_limit(max(lens), D)
+    rc = lib.fa_varlen_prefill_fp16(_p(qc), _p(kc), _p(vc), _p(o), _p(cuc), 3, 207, H, D, max(lens), row_limit, 1,
+                                    _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    assert_close(o, A.varlen_prefill(q, k, v, cu, max(lens), True), what="capi varlen")
+    # token eviction
+    Bt, Ht, Nt, Dt = 2, 3, 100, 64
+    kt, vt = randn(g, Bt, Ht, Nt, Dt), randn(g, Bt, Ht, Nt, Dt)
+    sc = torch.randn(Bt, Nt, generator=g)
+    ktc, vtc, scc = kt.cuda(), vt.cuda(), sc.cuda()
+    ko, vo = torch.empty_like(ktc), torch.empty_like(vtc)
+    mask = torch.empty(Bt, Nt, dtype=torch.int32, device="cuda")
+    rc = lib.fa_token_eviction(_p(ktc), _p(vtc), _p(scc), _p(ko), _p(vo), _p(mask), Bt, Ht, Nt, Dt, 30, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    rk, rv, rm = A.token_eviction(kt, vt, sc, 30)
+    assert torch.equal(mask.cpu(), rm) and torch.equal(ko.cpu(), rk) and torch.equal(vo.cpu(), rv)
+    # speculative verify
+    Bs, K, V = 3, 4, 1000
+    tp = torch.softmax(torch.randn(Bs, K + 1, V, generator=g), -1)
+    dp = torch.softmax(torch.randn(Bs, K, V, generator=g), -1)
+    tok = torch.randint(0, V, (Bs, K), generator=g)
+    rv_ = torch.rand(Bs, K, generator=g)
+    tpc, dpc, tokc, rvc = tp.cuda(), dp.cuda(), tok.cuda(), rv_.cuda()
+    acc = torch.empty(Bs, dtype=torch.int32, device="cuda")
+    out = torch.empty(Bs, K + 1, dtype=torch.int64, device="cuda")
+    rc = lib.fa_speculative_verify(_p(tpc), _p(dpc), _p(tokc), _p(rvc), _p(acc), _p(out), Bs, K, V, _st())
+    assert rc == FA_OK, lib.fa_last_error()
+    torch.cuda.synchronize()
+    racc, rout = A.speculative_verify(tp, dp, tok, rv_, K)
+    assert torch.equal(acc.cpu(), racc) and torch.equal(out.cpu(), rout)
+    # tensor-parallel helpers
+    full = randn(g, 2, 8, 33, 64)
+    fc = full.cuda()
+    loc = torch.empty(2, 3, 33, 64, dtype=torch.float16, device="cuda")
+    assert lib.fa_scatter_heads(_p(fc), _p(loc), 2, 8, 4, 3, 33, 64, _st()) == FA_OK
+    back = torch.zeros_like(fc)
+    assert lib.fa_gather_heads(_p(back), _p(loc), 2, 8, 4, 3, 33, 64, _st()) == FA_OK
+    d0 = randn(g, 5000)
+    dd, ss = d0.cuda(), randn(g, 5000).cuda()
+    s_cpu = ss.cpu()
+    assert lib.fa_cross_gpu_allreduce_fp16(_p(dd), _p(ss), ctypes.c_size_t(5000), _st()) == FA_OK
+    torch.cuda.synchronize()
+    assert torch.equal(loc.cpu(), full[:, 4:7])
+    assert torch.equal(back.cpu(), A.gather_heads(torch.zeros_like(full), loc.cpu(), 8, 4, 3))
+    assert torch.equal(dd.cpu(), A.allreduce_fp16(d0, s_cpu))
+    # argument errors of the TP helpers
+    assert lib.fa_scatter_heads(_p(fc), _p(loc), 2, 8, 6, 3, 33, 64, _st()) == FA_ERR_INVALID_ARG
