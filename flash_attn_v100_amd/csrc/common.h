@@ -189,6 +189,26 @@ __device__ __forceinline__ void copy16_to_lds(const half_t* base, unsigned lane_
       : "memory");
 }
 
+// copy16_to_lds with a nontemporal (streaming) read of data used once.
+__device__ __forceinline__ void copy16_to_lds_nt(const half_t* base, unsigned lane_off, unsigned lds_addr) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, %3 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(lane_off), "s"(base)
+      : "memory");
+}
+
+// s_waitcnt vmcnt(N) alone (LDS and scalar loads not waited for).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | (0xF << 8));
+}
+
 // As copy16_to_lds with 4 bytes per lane (global_load_lds_dword): lane i's
 // dword lands at lds_addr + 4 i.
 __device__ __forceinline__ void copy4_to_lds(const float* base, unsigned lane_off, unsigned lds_addr) {
