@@ -100,6 +100,29 @@ struct DecodeParams {
   float scale;                 // 1/sqrt(D) (INT8 score formula)
 };
 
+// Fetch the kernel arguments a mode uses at once: left to itself the compiler
+// loads them in dependent rounds behind the early exits, a memory round trip
+// each before the first key load can issue.
+template <int MODE>
+__device__ __forceinline__ void preload_args(const DecodeParams& p) {
+  asm volatile("" ::"s"(p.q), "s"(p.o), "s"(p.ws_o), "s"(p.ws_lse), "s"(p.counters), "s"(p.flags));
+  asm volatile("" ::"s"(p.use_flags), "s"(p.early_merge), "s"(p.unit_base), "s"(p.B), "s"(p.H_Q), "s"(p.H_KV),
+               "s"(p.N), "s"(p.D), "s"(p.G));
+  asm volatile("" ::"s"(p.chunk), "s"(p.num_splits), "s"(p.num_hg), "s"(p.absorb_tail), "s"(p.scale_log2));
+  if constexpr (MODE == kModeInt8KV) {
+    asm volatile("" ::"s"(p.k8), "s"(p.v8), "s"(p.k_sc), "s"(p.v_sc), "s"(p.fixed_len), "s"(p.seg1),
+                 "s"(p.seg_shift));
+  } else {
+    asm volatile("" ::"s"(p.k), "s"(p.v));
+  }
+  if constexpr (MODE == kModeInt8) asm volatile("" ::"s"(p.q_scale), "s"(p.k_scale), "s"(p.fixed_len), "s"(p.scale));
+  if constexpr (MODE == kModeDecode) asm volatile("" ::"s"(p.fixed_len), "s"(p.seg1), "s"(p.seg_shift));
+  if constexpr (MODE == kModeCB) asm volatile("" ::"s"(p.lens), "s"(p.lpt), "s"(p.seg1), "s"(p.seg_shift));
+  if constexpr (MODE == kModePaged)
+    asm volatile("" ::"s"(p.lens), "s"(p.lpt), "s"(p.block_table), "s"(p.bt_numel), "s"(p.max_num_blocks),
+                 "s"(p.num_pages));
+}
+
 template <int MODE>
 __device__ __forceinline__ int seq_len_of(const DecodeParams& p, int b) {
   if constexpr (MODE == kModeCB) {
@@ -207,6 +230,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   constexpr int GP = PExchange<GB>::kPad;     // padded heads per key in the exchange
   constexpr float kRescaleSlack = 8.0f;       // log2 headroom before the max is refreshed
   static_assert(TK % RPW == 0, "tile");
+  preload_args<MODE>(p);
 
   const int S = p.num_splits;
   const int split = blockIdx.x % S;

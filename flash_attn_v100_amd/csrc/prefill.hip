@@ -82,6 +82,9 @@ struct PrefillParams {
 #ifndef FA_PRE_W64
 #define FA_PRE_W64 4
 #endif
+#ifndef FA_PRE_NSW
+#define FA_PRE_NSW 4
+#endif
 #ifndef FA_PRE_NS128
 #define FA_PRE_NS128 3
 #endif
@@ -90,17 +93,26 @@ struct PrefillParams {
 #endif
 // WIDE (D <= 64 only): 64-key tiles for launches of at most about one
 // residency round of workgroups, where fewer, longer tiles per barrier win
-// (measured 5-12 % on N <= 1024); larger launches keep 32-key tiles.
-template <int DP, bool WIDE = false>
+// (measured 5-12 % on N <= 1024); larger launches keep 32-key tiles.  Their
+// ring has 4 stages, so three tiles are in flight from the start (short
+// sequences: most of the keys).
+//
+// KSPLIT (D <= 128, launches far smaller than the chip): the four waves share
+// one 32-row query block and split every 128-key tile, wave w taking keys
+// 32w .. 32w + 31; their partial (max, sum, O) merge through LDS at the end.
+// Each wave's serial chain is then a quarter of the keys, which is what bounds
+// short prefills that occupy only a few dozen CUs.
+template <int DP, bool WIDE = false, bool KSPLIT = false>
 struct PrefillShape {
-  static constexpr int RB = DP <= 64 ? FA_PRE_RB64 : 1;                 // 32-row query blocks per wave
+  static constexpr int RB = KSPLIT ? 1 : (DP <= 64 ? FA_PRE_RB64 : 1);  // 32-row query blocks per wave
   static constexpr int RW = 32 * RB;                                    // query rows per wave
-  static constexpr int BQ = kPreWaves * RW;                             // query rows per workgroup
-  static constexpr int BK = DP <= 64 ? (WIDE ? 64 : FA_PRE_BK64) : 32;  // keys per tile
-  static constexpr int NS = DP <= 64 ? 3 : (DP <= 128 ? FA_PRE_NS128 : 2);  // LDS ring stages
+  static constexpr int BQ = KSPLIT ? RW : kPreWaves * RW;               // query rows per workgroup
+  static constexpr int BK = KSPLIT ? 32 * kPreWaves : (DP <= 64 ? (WIDE ? 64 : FA_PRE_BK64) : 32);  // keys per tile
+  static constexpr int NS = KSPLIT ? (DP <= 64 ? 3 : 2)
+                                   : (DP <= 64 ? (WIDE ? FA_PRE_NSW : 3) : (DP <= 128 ? FA_PRE_NS128 : 2));  // LDS ring stages
   static constexpr int TILE = BK * DP;                                  // halves per K (or V) tile
   static constexpr int WAVES_PER_SIMD =
-      DP <= 64 ? (WIDE ? 3 : FA_PRE_W64) : (DP <= 128 ? FA_PRE_W128 : 2);  // register budget target
+      KSPLIT ? 2 : (DP <= 64 ? (WIDE ? 3 : FA_PRE_W64) : (DP <= 128 ? FA_PRE_W128 : 2));  // register budget target
 };
 
 // Varlen output rows that no sequence's attention writes are set to zero by
@@ -136,17 +148,23 @@ __device__ void zero_unwritten_rows(const PrefillParams& p, int z) {
   }
 }
 
-template <int DP, bool VARLEN, bool VEC, bool WIDE = false>
+__device__ __forceinline__ void preload_args(const PrefillParams& p) {
+  asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.o), "s"(p.lse), "s"(p.cu_seqlens));
+  asm volatile("" ::"s"(p.B), "s"(p.H_Q), "s"(p.H_KV), "s"(p.N), "s"(p.D), "s"(p.G), "s"(p.total), "s"(p.row_limit));
+  asm volatile("" ::"s"(p.causal), "s"(p.qtiles), "s"(p.zero_base), "s"(p.group_units), "s"(p.scale_log2));
+}
+
+template <int DP, bool VARLEN, bool VEC, bool WIDE = false, bool KSPLIT = false>
 __global__ __launch_bounds__(kPreThreads)
-__attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) void prefill_kernel(PrefillParams p) {
-  using Shape = PrefillShape<DP, WIDE>;
+__attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE, KSPLIT>::WAVES_PER_SIMD))) void prefill_kernel(PrefillParams p) {
+  using Shape = PrefillShape<DP, WIDE, KSPLIT>;
   constexpr int RB = Shape::RB;
   constexpr int RW = Shape::RW;
   constexpr int BQ = Shape::BQ;
   constexpr int kBK = Shape::BK;
   constexpr int NS = Shape::NS;
   constexpr int TILE = Shape::TILE;
-  constexpr int NBLK = kBK / 32;              // 32-key blocks per tile
+  constexpr int NBLK = KSPLIT ? 1 : kBK / 32;  // 32-key blocks per tile computed by one wave
   constexpr int KK = DP / 16;                 // 16-wide d slices of QK^T
   constexpr int DB = DP / 32;                 // 32-row d blocks of PV
   constexpr int CPR = DP / 8;                 // 16-byte chunks per row
@@ -156,6 +174,10 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
 
   __shared__ __attribute__((aligned(1024))) half_t smem[NS * 2 * Shape::TILE];
 
+  // Fetch every kernel argument at once: left to itself the compiler loads
+  // them in several dependent rounds behind the early exits, each a memory
+  // round trip before the first tile copy can issue.
+  preload_args(p);
   const int D = p.D;
   if constexpr (VARLEN) {
     if (static_cast<int>(blockIdx.x) >= p.zero_base) {
@@ -221,7 +243,8 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
-  const int wq0 = q0 + wave * RW;  // first query row of this wave
+  const int wq0 = q0 + (KSPLIT ? 0 : wave * RW);  // first query row of this wave
+  const int kw = KSPLIT ? 32 * wave : 0;            // first key of this wave's block inside a tile
 
   const half_t* __restrict__ qp = p.q + q_base;
   const half_t* __restrict__ kp = p.k + k_base;
@@ -270,8 +293,9 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
       }
     }
   };
-  if (ntiles > 0) issue(0);
-  if (NS > 2 && ntiles > 1) issue(1);
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < ntiles) issue(t);
 
   // ---- Q fragments: B operand of S^T; block rb, lane row wq0 + 32 rb + l32, d = 16 kk + 8 hi .. +8 ----
   half8_t qf[RB][KK];
@@ -316,9 +340,9 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
       (v_row * DP + (((2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1)) ^ v_sw) * 8) + (s16 & 1) * 4) * sizeof(half_t);
 
   auto compute_tile = [&](const int t, const bool masked) {
-    const int kt = t * kBK;
-    const unsigned kaddr = lds_base + (t % NS) * kStageBytes + k_lane;
-    const unsigned vaddr = lds_base + (t % NS) * kStageBytes + kTileBytes + v_lane;
+    const int kt = t * kBK + kw;  // first key of the wave's keys in this tile
+    const unsigned kaddr = lds_base + (t % NS) * kStageBytes + k_lane + kw * DP * 2;
+    const unsigned vaddr = lds_base + (t % NS) * kStageBytes + kTileBytes + v_lane + kw * DP * 2;
     // ---- S^T = K Q^T ----
     float16_t sacc[NBLK][RB];
 #pragma unroll
@@ -342,14 +366,18 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
       if (masked) {  // uniform: only tiles crossing the diagonal or the sequence end
+        // Element r of block blk holds key kt + 4 hi + off (off = 32 blk +
+        // 8 (r / 4) + r % 4, a constant); it is dead past the lane's last live
+        // key, so one compare against a per-lane bound masks it.
         const int qrow = wq0 + 32 * rb + l32;
+        const int last = p.causal ? min(qrow, seq_len - 1) : seq_len - 1;
+        const int bound = last - kt - 4 * hi;  // live iff off <= bound
 #pragma unroll
         for (int blk = 0; blk < NBLK; ++blk)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int key = kt + blk * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
-            const bool dead = key >= seq_len || (p.causal && key > qrow);
-            sacc[blk][rb][r] = dead ? -INFINITY : sacc[blk][rb][r];
+            const int off = blk * 32 + 8 * (r >> 2) + (r & 3);
+            sacc[blk][rb][r] = off > bound ? -INFINITY : sacc[blk][rb][r];
           }
       }
       // p = exp2(s c - m) against the running max m.  A lane's partial sum can
@@ -369,7 +397,8 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
         }
         return ls;
       };
-      float ls = exponentiate(-m_run[rb]);
+      // Tile 0 always sets the max (m = -1e30 before it): skip the trial pass.
+      float ls = t == 0 ? 2.0f * kRescaleLimit : exponentiate(-m_run[rb]);
       if (__builtin_amdgcn_ballot_w64(ls > kRescaleLimit) != 0) {
         float mx = sacc[0][rb][0];
 #pragma unroll
@@ -412,15 +441,91 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
 
   for (int t = 0; t < ntiles; ++t) {
     // this wave's copies of tile t have landed (tile t+1 may still be in flight)
-    if (VEC && NS > 2 && t + 1 < ntiles)
+    if (VEC && NS > 3 && t + 2 < ntiles)
+      wait_vm_lgkm0<4 * IPW>();
+    else if (VEC && NS > 2 && t + 1 < ntiles)
       wait_vm_lgkm0<2 * IPW>();
     else
       wait_vm_lgkm0<0>();
     tile_barrier();  // every wave's copies of tile t landed; stage (t-1) % NS is free
     if (t + NS - 1 < ntiles) issue(t + NS - 1);
-    const int kt = t * kBK;
+    const int kt = t * kBK + kw;
+    constexpr int kWaveKeys = KSPLIT ? 32 : kBK;  // keys of a tile this wave computes
     if (kt >= kend_w) continue;  // past this wave's diagonal (still copies and joins the barriers)
-    compute_tile(t, (kt + kBK > seq_len) || (p.causal && kt + kBK - 1 > wq0));
+    compute_tile(t, (kt + kWaveKeys > seq_len) || (p.causal && kt + kWaveKeys - 1 > wq0));
+  }
+
+  if constexpr (KSPLIT) {
+    // ---- merge the four waves' partials of the shared 32 rows ----
+    // Lane (l32, hi) holds O[l32][32 db + 8 rr + 4 hi + j] = oacc[db][0][4 rr + j]
+    // against its wave's max m; scaled to the common max M, the waves' O and
+    // l add up.  A wave that saw no key keeps m = -1e30 and weighs 0.
+    __shared__ float s_mw[kPreWaves][32];
+    __shared__ float s_lw[kPreWaves][32];
+    __syncthreads();  // every wave is done reading the ring
+    // [wave][32 rows][DP + 4] fp32: the 16-byte row pad spreads the 32 rows
+    // of one column block over distinct banks
+    constexpr int RS = DP + 4;
+    float* red = reinterpret_cast<float*>(smem);
+    if (hi == 0) s_mw[wave][l32] = m_run[0];
+    __syncthreads();
+    float mx = s_mw[0][l32];
+#pragma unroll
+    for (int w = 1; w < kPreWaves; ++w) mx = fmaxf(mx, s_mw[w][l32]);
+    const float alpha = fast_exp2(m_run[0] - mx);
+    const float lw = (l_run[0] + __shfl_xor(l_run[0], 32, 64)) * alpha;
+    if (hi == 0) s_lw[wave][l32] = lw;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float4_t x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) x[j] = oacc[db][0][4 * rr + j] * alpha;
+        *reinterpret_cast<float4_t*>(red + (wave * 32 + l32) * RS + db * 32 + 8 * rr + 4 * hi) = x;
+      }
+    __syncthreads();
+    // thread: row tid / 8, columns (tid % 8) * DP / 8 .. + DP / 8
+    constexpr int CPT = DP / 8;
+    const int r = tid >> 3;
+    const int c0 = (tid & 7) * CPT;
+    const int qrow = q0 + r;
+    if (qrow < rows) {
+      float lt = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kPreWaves; ++w) lt += s_lw[w][r];
+      const float inv = 1.0f / lt;
+      if constexpr (!VARLEN) {
+        if (p.lse != nullptr && (tid & 7) == 0) {
+          float m = s_mw[0][r];
+#pragma unroll
+          for (int w = 1; w < kPreWaves; ++w) m = fmaxf(m, s_mw[w][r]);
+          p.lse[(static_cast<size_t>(b) * p.H_Q + h) * p.N + qrow] = (m + log2f(lt)) * 0.69314718055994531f;
+        }
+      }
+      half_t* op = p.o + q_base + static_cast<size_t>(qrow) * stride;
+#pragma unroll
+      for (int c = 0; c < CPT; c += 4) {
+        float4_t acc = *reinterpret_cast<const float4_t*>(red + r * RS + c0 + c);
+#pragma unroll
+        for (int w = 1; w < kPreWaves; ++w) {
+          const float4_t y = *reinterpret_cast<const float4_t*>(red + (w * 32 + r) * RS + c0 + c);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[j] += y[j];
+        }
+        half4_t hv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hv[j] = static_cast<half_t>(acc[j] * inv);
+        if constexpr (VEC) {
+          *reinterpret_cast<half4_t*>(op + c0 + c) = hv;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (c0 + c + j < D) op[c0 + c + j] = hv[j];
+        }
+      }
+    }
+    return;
   }
 
   // ---- finalize and store O[qrow][d] ----
@@ -457,14 +562,20 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE>::WAVES_PER_SIMD))) voi
   }
 }
 
-template <int DP, bool VARLEN, bool WIDE = false>
+template <int DP, bool VARLEN, bool WIDE = false, bool KSPLIT = false>
 static void launch_prefill(bool vec, int blocks, const PrefillParams& p, hipStream_t st) {
   if (vec)
-    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, true, WIDE>), dim3(blocks), dim3(kPreThreads), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, true, WIDE, KSPLIT>), dim3(blocks), dim3(kPreThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, false, WIDE>), dim3(blocks), dim3(kPreThreads), 0, st, p);
+    hipLaunchKernelGGL((prefill_kernel<DP, VARLEN, false, WIDE, KSPLIT>), dim3(blocks), dim3(kPreThreads), 0, st, p);
 }
 constexpr long long kWideMaxBlocks = 1024;  // D <= 64 launches up to this size use 64-key tiles
+// D <= 128 launches of at most this many 128-row workgroups run key-split
+// (four times as many 32-row workgroups).
+#ifndef FA_PRE_KSPLIT_MAX
+#define FA_PRE_KSPLIT_MAX 64
+#endif
+constexpr long long kKsplitMaxBlocks = FA_PRE_KSPLIT_MAX;
 
 static int prefill_bq(int D) { return D <= 64 ? PrefillShape<64>::BQ : (D <= 128 ? PrefillShape<128>::BQ : PrefillShape<256>::BQ); }
 
@@ -472,7 +583,8 @@ static int prefill_bq(int D) { return D <= 64 ? PrefillShape<64>::BQ : (D <= 128
 // tail); returns FA_OK or an error code.
 template <bool VARLEN>
 static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, PrefillParams p, hipStream_t st) {
-  p.qtiles = ceil_div(rows_max, prefill_bq(D));
+  const bool ksplit = D <= 128 && static_cast<long long>(ceil_div(rows_max, prefill_bq(D))) * p.H_Q * p.B <= kKsplitMaxBlocks;
+  p.qtiles = ceil_div(rows_max, ksplit ? PrefillShape<64, false, true>::BQ : prefill_bq(D));
 #if FA_PRE_ORDER == 0
   const long long main_blocks = static_cast<long long>(p.qtiles) * p.H_Q * p.B;
 #else
@@ -487,7 +599,10 @@ static int dispatch_prefill(const char* fn, int D, bool vec, int rows_max, Prefi
   if (blocks > 0x7fffffffLL) return set_error(FA_ERR_UNSUPPORTED, "%s: problem too large for one launch", fn);
   if (blocks == 0) return FA_OK;
   p.zero_base = static_cast<int>(main_blocks);
-  if (D <= 64) {
+  if (ksplit) {
+    if (D <= 64) launch_prefill<64, VARLEN, false, true>(vec, static_cast<int>(blocks), p, st);
+    else launch_prefill<128, VARLEN, false, true>(vec, static_cast<int>(blocks), p, st);
+  } else if (D <= 64) {
     if (main_blocks <= kWideMaxBlocks) launch_prefill<64, VARLEN, true>(vec, static_cast<int>(blocks), p, st);
     else launch_prefill<64, VARLEN>(vec, static_cast<int>(blocks), p, st);
   }
