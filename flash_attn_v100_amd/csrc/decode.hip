@@ -419,10 +419,10 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // lane, so the MFMA-layout reads (16 lanes = 16 rows at one chunk) hit 16
   // distinct bank groups.  Each wave owns its tile: no barriers.
   constexpr bool kLdsK = (MODE == kModeCB || MODE == kModePaged) && VEC;
-  // Continuous-batching and paged caches are read once per call: nontemporal
-  // loads (measured 11 % faster on the paged cache, whose 4 KB page blocks
-  // would otherwise fill L2 with lines never read again).
-  constexpr bool kStreamKV = MODE == kModeCB || MODE == kModePaged;
+  // Every fp16 cache is read once per call: nontemporal loads (measured 11 %
+  // faster on the paged cache, 2-3 % on contiguous and INT8 decode; the int8
+  // cache's 8-byte V loads measured 8 % slower with them).
+  constexpr bool kStreamKV = MODE != kModeInt8KV;
   constexpr int CPR = DP / 8;                   // 16-byte chunks per key row
   constexpr int KCOPIES = TK * CPR / 64;        // copies per lane per tile
   constexpr int RPC = 64 / CPR;                 // key rows per copy instruction
@@ -451,7 +451,8 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
           const half_t* kh = p.k + kv_head_base;
           const int t = min(t0 + r, klast);
           const int row = t < p.seg1 ? t : t + p.seg_shift;
-          copy16_to_lds_nt(kh, static_cast<unsigned>((row * D + lc * 8) * 2), dst);
+          const unsigned off = static_cast<unsigned>((row * D + lc * 8) * 2);
+          if constexpr (kStreamKV) copy16_to_lds_nt(kh, off, dst); else copy16_to_lds(kh, off, dst);
         }
       }
     }
