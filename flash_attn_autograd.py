@@ -16,7 +16,7 @@ class FlashAttentionFunction(torch.autograd.Function):
         elif q.dtype == torch.float32:
             out, lse = flash_attn_v100.forward_with_lse(q, k, v, causal)
         else:
-            raise TypeError("flash_attn only supports float16 and float32")
+            raise TypeError(f"flash_attn: q must be torch.float16 or torch.float32, got {q.dtype}")
         ctx.save_for_backward(q, k, v, out, lse)
         ctx.causal = causal
         return out
