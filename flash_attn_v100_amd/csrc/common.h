@@ -171,6 +171,18 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70);
 }
 
+// A wave-uniform pointer as SGPRs (readfirstlane of both halves): the copy
+// helpers below take their base as an asm "s" operand, which does not
+// compile when the compiler cannot prove the value uniform; for a value
+// already in SGPRs this costs nothing.
+template <typename T>
+__device__ __forceinline__ const T* sgpr_ptr(const T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // One 16-byte-per-lane copy HBM -> LDS (global_load_lds_dwordx4, scalar base +
 // 32-bit lane byte offset): lane i's 16 bytes land at LDS byte address
 // lds_addr + 16 i.  Issued from asm so that the compiler does not track the
@@ -185,7 +197,7 @@ __device__ __forceinline__ void copy16_to_lds(const half_t* base, unsigned lane_
       "global_load_lds_dwordx4 %2, %3\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "s"(lds_addr), "v"(lane_off), "s"(base)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_off), "s"(sgpr_ptr(base))
       : "memory");
 }
 
@@ -198,7 +210,7 @@ __device__ __forceinline__ void copy16_to_lds_nt(const half_t* base, unsigned la
       "global_load_lds_dwordx4 %2, %3 nt\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "s"(lds_addr), "v"(lane_off), "s"(base)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_off), "s"(sgpr_ptr(base))
       : "memory");
 }
 
@@ -219,7 +231,7 @@ __device__ __forceinline__ void copy4_to_lds(const float* base, unsigned lane_of
       "global_load_lds_dword %2, %3\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "s"(lds_addr), "v"(lane_off), "s"(base)
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_off), "s"(sgpr_ptr(base))
       : "memory");
 }
 

@@ -45,8 +45,6 @@ constexpr int kPage = 16;             // PAGE_BLOCK_SIZE of the paged cache
 #define FA_DEC_CHUNK_QUANTUM 256
 #endif
 constexpr unsigned kCounterSlotsDev = 65536;  // arrival counters in the workspace
-// Polls of one ready flag before the merging split gives up (about 0.1 s).
-constexpr unsigned kMergeSpinLimit = 1u << 20;
 constexpr int kMaxChunk = 8192;                        // keys per split, upper bound
 constexpr int kChunkQuantum = FA_DEC_CHUNK_QUANTUM;    // split boundaries are multiples of this
 constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many split workgroups
@@ -84,9 +82,6 @@ struct DecodeParams {
   float* ws_o;                 // [B*H_Q, S, DP] normalised partial outputs
   float* ws_lse;               // [B*H_Q, S] log2-sum-exp of each partial
   unsigned* counters;          // [2 * kCounterSlots] arrivals, then publications, per unit; zero between calls
-  unsigned* flags;             // [kFlagWords] per-split ready flags (slot * S + split); zero between calls
-  int use_flags;               // this launch publishes through flags (units * S <= kFlagWords)
-  int early_merge;             // arrival ranks at the start, merger waits for publication
   int unit_base;               // first unit of this launch
   int B, H_Q, H_KV, N, D, G;
   int fixed_len;               // decode / INT8: number of attended keys
@@ -105,8 +100,8 @@ struct DecodeParams {
 // each before the first key load can issue.
 template <int MODE>
 __device__ __forceinline__ void preload_args(const DecodeParams& p) {
-  asm volatile("" ::"s"(p.q), "s"(p.o), "s"(p.ws_o), "s"(p.ws_lse), "s"(p.counters), "s"(p.flags));
-  asm volatile("" ::"s"(p.use_flags), "s"(p.early_merge), "s"(p.unit_base), "s"(p.B), "s"(p.H_Q), "s"(p.H_KV),
+  asm volatile("" ::"s"(p.q), "s"(p.o), "s"(p.ws_o), "s"(p.ws_lse), "s"(p.counters));
+  asm volatile("" ::"s"(p.unit_base), "s"(p.B), "s"(p.H_Q), "s"(p.H_KV),
                "s"(p.N), "s"(p.D), "s"(p.G));
   asm volatile("" ::"s"(p.chunk), "s"(p.num_splits), "s"(p.num_hg), "s"(p.absorb_tail), "s"(p.scale_log2));
   if constexpr (MODE == kModeInt8KV) {
@@ -305,13 +300,6 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
 
   // Splits that hold keys of this sequence (>= 1 here, since k0 < k1).
   const int sb = min(S, (L + p.chunk - 1) / p.chunk);
-  // Early merge (small grids): the arrival rank among the unit's splits is
-  // taken now, so the atomic's round trip overlaps the key loads, and the
-  // split that arrives last merges, waiting for the others to publish.
-  // Otherwise the rank is taken once the partial is written, and the split
-  // that finishes last merges without waiting.
-  unsigned arrival = 0;
-  if (p.early_merge && sb > 1 && tid == 0) arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
 
   // Paged: the page ids of the keys [r0, r1) being walked are staged in LDS,
   // kMaxChunk keys per round (one round unless the sequence overruns its
@@ -822,24 +810,15 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // ---- publish this split's partial; the last-arriving split merges ----
   // Partials travel through device-coherent (L2-bypassing, sc1) stores and
   // loads, so no whole-L2 writeback/invalidate fence is needed.  Once all of
-  // a split's partial stores are complete it publishes them: with ready
-  // flags (launches of at most kFlagWords unit splits) it sets its own flag,
-  // otherwise it bumps the unit's publication counter.  The split with the
-  // last arrival rank waits until every split of the unit has published, then
-  // merges.  That wait always ends: each split that took an arrival rank
-  // before the merger is already running and needs nothing from anyone.  It
-  // is bounded all the same; past the bound the merger writes NaN.
-  __shared__ int s_last, s_timeout;
+  // a split's partial stores are complete it takes its arrival rank on the
+  // unit's counter; the split with the last rank finds every other partial
+  // complete and merges at once.
+  __shared__ int s_last;
   wait_vmem_stores();
   __syncthreads();
-  unsigned* published = &p.counters[kCounterSlotsDev + counter_index(slot)];
-  unsigned* flags = p.flags + static_cast<size_t>(slot) * S;
   if (tid == 0) {
-    if (!p.early_merge) arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
-    else if (p.use_flags) __hip_atomic_store(&flags[split], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else __hip_atomic_fetch_add(published, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
     s_last = (arrival == static_cast<unsigned>(sb - 1));
-    s_timeout = 0;
   }
   __syncthreads();
   if (!s_last) return;
@@ -849,19 +828,13 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
 
   // ---- merge ----
   // Thread (column group c, phase ph) merges 4 output columns over the splits
-  // ph, ph + NPH, ... .  When they fit one batch (sb <= NB * NPH) the loads
-  // go in two rounds, in the same registers: first the splits already
-  // published when the merger gets here (most of them, read while the
-  // stragglers still run), then, once every split has published, the rest.
-  // The combine runs after both, in split order, so the result does not
-  // depend on which round a split fell in.  Larger sb: batches after all
-  // splits have published.  Partials are read with device-coherent (sc1)
-  // buffer loads.
+  // ph, ph + NPH, ..., in batches of NB loads, in split order (the result
+  // does not depend on the arrival order).  Partials are read with
+  // device-coherent (sc1) buffer loads.
   constexpr int NP = GB * DP / 4;                                  // float4 columns
   constexpr int NPH = NP >= kDecThreads ? 1 : kDecThreads / NP;    // split phases
   constexpr int NB = 16;                                           // splits per load batch
   constexpr int NCOL = (NP + kDecThreads - 1) / kDecThreads;       // columns per thread
-  __shared__ unsigned long long s_ready[2];  // splits loaded in the first round
   __shared__ float4_t s_num[NPH][NPH > 1 ? NP : 1];
   __shared__ float s_mx[NPH][NPH > 1 ? NP : 1];
   __shared__ float s_den[NPH][NPH > 1 ? NP : 1];
@@ -899,120 +872,37 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
     }
     r.mx = m;
   };
-  // Waits until every split has published (flags: wave 0, a lane per split,
-  // skipping those seen in the first round; counter: one thread).
-  auto wait_all = [&](unsigned long long seen0, unsigned long long seen1) {
-    if (p.use_flags) {
-      if (wave == 0) {
-        for (int h = 0; h < 2; ++h) {
-          const int sp = lane + 64 * h;
-          if (sp < sb && !(((h ? seen1 : seen0) >> lane) & 1ull)) {
-            unsigned spins = 0;
-            while (__hip_atomic_load(&flags[sp], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-              if (++spins > kMergeSpinLimit) {
-                s_timeout = 1;
-                break;
-              }
-              __builtin_amdgcn_s_sleep(1);
-            }
-          }
-        }
-      }
-    } else if (tid == 0) {
-      unsigned spins = 0;
-      while (__hip_atomic_load(published, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < static_cast<unsigned>(sb)) {
-        if (++spins > kMergeSpinLimit) {
-          s_timeout = 1;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-    }
-    __syncthreads();
-    // Every split has published: leave the flags (or the publication
-    // counter) at zero for the next call on this workspace now, so the stores
-    // overlap the merge instead of delaying the kernel's end.
-    if (p.use_flags) {
-      if (tid < sb) __hip_atomic_store(&flags[tid], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else if (tid == 0) {
-      __hip_atomic_store(published, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  };
   const int c_mine = NPH > 1 ? tid % NP : tid;
   const int ph = NPH > 1 ? tid / NP : 0;
   Part parts[NCOL];
 #pragma unroll
   for (int q = 0; q < NCOL; ++q) parts[q] = Part{float4_t{0.0f, 0.0f, 0.0f, 0.0f}, -INFINITY, 0.0f};
-  if (p.early_merge && NCOL == 1 && sb <= NB * NPH) {
-    // first round: the splits published so far
-    unsigned long long r0 = 0, r1 = 0;
-    if (p.use_flags && wave == 0) {
-      const bool f0 = lane < sb && __hip_atomic_load(&flags[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-      const bool f1 =
-          lane + 64 < sb && __hip_atomic_load(&flags[lane + 64], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-      r0 = __builtin_amdgcn_ballot_w64(f0);
-      r1 = __builtin_amdgcn_ballot_w64(f1);
-      if (lane == 0) {
-        s_ready[0] = r0;
-        s_ready[1] = r1;
-      }
-    } else if (!p.use_flags && tid == 0) {
-      s_ready[0] = s_ready[1] = 0ull;
-    }
-    __syncthreads();
-    const unsigned long long m0 = s_ready[0], m1 = s_ready[1];
-    auto ready = [&](int sp) { return ((sp < 64 ? m0 : m1) >> (sp & 63)) & 1ull; };
-    const bool active = ph < NPH && ph < sb && column_ok(c_mine);
-    float4_t v[NB];
-    float lv[NB];
+  if (ph < NPH) {
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      lv[j] = -INFINITY;
-      const int sp = ph + j * NPH;
-      if (active && sp < sb && ready(sp)) load_split(c_mine, sp, v[j], lv[j]);
-    }
-    // second round: the rest, once published.  The first round's loads are
-    // completed first (they had the wait to land), so the second round's
-    // loads into the same registers need no wait of their own.
-    wait_all(m0, m1);
-    wait_vmem();
+    for (int q = 0; q < NCOL; ++q) {
+      const int c = c_mine + q * kDecThreads;
+      if (!column_ok(c)) continue;
+      for (int k0 = ph; k0 < sb; k0 += NB * NPH) {
+        float4_t v[NB];
+        float lv[NB];
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const int sp = ph + j * NPH;
-      if (active && sp < sb && !ready(sp)) load_split(c_mine, sp, v[j], lv[j]);
-    }
-    if (active) combine(parts[0], v, lv);
-  } else {
-    if (p.early_merge) wait_all(0ull, 0ull);
-    if (ph < NPH) {
-#pragma unroll
-      for (int q = 0; q < NCOL; ++q) {
-        const int c = c_mine + q * kDecThreads;
-        if (!column_ok(c)) continue;
-        for (int k0 = ph; k0 < sb; k0 += NB * NPH) {
-          float4_t v[NB];
-          float lv[NB];
-#pragma unroll
-          for (int j = 0; j < NB; ++j) {
-            v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-            lv[j] = -INFINITY;
-            const int sp = k0 + j * NPH;
-            if (sp < sb) load_split(c, sp, v[j], lv[j]);
-          }
-          combine(parts[q], v, lv);
+        for (int j = 0; j < NB; ++j) {
+          v[j] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          lv[j] = -INFINITY;
+          const int sp = k0 + j * NPH;
+          if (sp < sb) load_split(c, sp, v[j], lv[j]);
         }
+        combine(parts[q], v, lv);
       }
     }
   }
-  const bool timed_out = s_timeout != 0;
 
   auto store_out = [&](int c, float4_t o) {
     const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
     half_t* op = p.o + (unit_bh + g) * D + d4;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (d4 + j < D) op[j] = static_cast<half_t>(timed_out ? __builtin_nanf("") : o[j]);
+      if (d4 + j < D) op[j] = static_cast<half_t>(o[j]);
   };
   if constexpr (NPH == 1) {
 #pragma unroll
@@ -1085,32 +975,27 @@ static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int ta
 
 static size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-// Workspace layout: [counters: 2 x kCounterSlots u32][flags: kFlagWords u32][lse: B*H_Q*S f32]
-// [partials: B*H_Q*S*DP f32],
-// each region 256-byte aligned.  Needed only when a sequence can span several
-// splits.  The counter and flag regions have the same size and place for every
-// call, so one workspace can serve calls of any shape: no call's partials ever
-// land on another call's counters or flags.  A launch covers at most kCounterSlots units; larger
-// problems are issued as several launches over unit ranges.
+// Workspace layout: [arrival counters: kCounterSlots u32][lse: B*H_Q*S f32]
+// [partials: B*H_Q*S*DP f32], each region 256-byte aligned.  Needed only when
+// a sequence can span several splits.  The counter region has the same size
+// and place for every call, so one workspace can serve calls of any shape: no
+// call's partials ever land on another call's counters.  A launch covers at
+// most kCounterSlots units; larger problems are issued as several launches
+// over unit ranges.
 constexpr size_t kCounterSlots = kCounterSlotsDev;
-// The counter region holds kCounterSlots arrival counters, then as many
-// publication counters.
-constexpr size_t kCounterWords = 2 * kCounterSlots;
-// Per-split ready flags, used by launches whose units x splits fit.
-constexpr size_t kFlagWords = 65536;
+constexpr size_t kCounterWords = kCounterSlots;
 
 struct WorkspaceLayout {
-  size_t counters, flags, lse, o, total;
+  size_t counters, lse, o, total;
 };
 
 static WorkspaceLayout plan_layout(const DecodePlan& pl, int B, int H_Q, int H_KV) {
   (void)H_KV;
-  WorkspaceLayout w = {0, 0, 0, 0, 0};
+  WorkspaceLayout w = {0, 0, 0, 0};
   if (pl.splits <= 1) return w;
   const size_t entries = static_cast<size_t>(B) * H_Q * pl.splits;
   w.counters = 0;
-  w.flags = align256(kCounterWords * sizeof(unsigned));
-  w.lse = w.flags + align256(kFlagWords * sizeof(unsigned));
+  w.lse = align256(kCounterWords * sizeof(unsigned));
   w.o = w.lse + align256(entries * sizeof(float));
   w.total = w.o + entries * pl.dp * sizeof(float);
   return w;
@@ -1163,7 +1048,7 @@ static int target_blocks() {
 // kFixedQuantum keys; when that leaves CUs idle (fewer split workgroups than
 // kSmallGridBlocks) they split at kSmallGridQuantum instead: one 32-key tile
 // per wave, every load of the call issued at once (config 2: 16 -> 32 splits
-// per head, 128 -> 256 workgroups).
+// per head, 128 -> 256 workgroups; 64-key splits or none measured slower).
 constexpr int kSmallGridQuantum = kDecWaves * 32;
 constexpr long long kSmallGridBlocks = 256;
 
@@ -1201,7 +1086,6 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   if (need > 0) {
     char* base = static_cast<char*>(ws);
     p.counters = reinterpret_cast<unsigned*>(base + wl.counters);
-    p.flags = reinterpret_cast<unsigned*>(base + wl.flags);
     p.ws_lse = reinterpret_cast<float*>(base + wl.lse);
     p.ws_o = reinterpret_cast<float*>(base + wl.o);
   }
@@ -1213,8 +1097,6 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   for (long long u0 = 0; u0 < units; u0 += static_cast<long long>(kCounterSlots)) {
     const long long nu = units - u0 < static_cast<long long>(kCounterSlots) ? units - u0 : kCounterSlots;
     p.unit_base = static_cast<int>(u0);
-    p.use_flags = nu * pl.splits <= static_cast<long long>(kFlagWords) ? 1 : 0;
-    p.early_merge = nu * pl.splits <= kSmallGridBlocks ? 1 : 0;
     dispatch<MODE>(pl, vec, p, static_cast<int>(nu * pl.splits), st);
     const int rc = check_launch(fn);
     if (rc != FA_OK) return rc;
@@ -1263,8 +1145,8 @@ extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void*
 // its own copy until the process ends).  Host code never uses its name as an
 // address: the device address comes from hipGetSymbolAddress, once per device
 // with that device current, and only that pointer is passed to kernels or
-// memory calls.  The regions the kernels expect at zero (arrival and
-// publication counters, ready flags) start at zero (static storage, and a
+// memory calls.  The region the kernels expect at zero (the arrival
+// counters) starts at zero (static storage, and a
 // synchronous clear at set-up when the first call is not being captured),
 // and every call leaves them at zero.  Calls that overlap on one GPU share
 // the array and race.
@@ -1296,7 +1178,7 @@ int static_scratch(const char* fn, void* stream, void** out) {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cap) == hipSuccess &&
         cap == hipStreamCaptureStatusNone) {
-      const size_t zero_bytes = kCounterWords * sizeof(unsigned) + kFlagWords * sizeof(unsigned) + 512;
+      const size_t zero_bytes = align256(kCounterWords * sizeof(unsigned));
       slot.err = hipMemset(ptr, 0, zero_bytes);
     }
   });
