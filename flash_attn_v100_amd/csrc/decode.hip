@@ -686,6 +686,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
       } else {
         load_tile(A, t0);
       }
+      // Contiguous decode: every load of the tile is issued before any of its
+      // arithmetic (left to itself the scheduler put the first QK^T MFMA, and
+      // its wait for Q and the first K rows, ahead of the V loads; config 2
+      // 9.2 -> 9.05 us).  The INT8 modes measured slower with it (5b +4 %).
+      if constexpr (MODE == kModeDecode) __builtin_amdgcn_sched_barrier(0);
       compute_tile(A, t0);
     }
   };
