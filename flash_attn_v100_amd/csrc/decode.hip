@@ -1,26 +1,29 @@
 // Split-KV ("flash-decoding") single-token attention for gfx950.
 //
-// One kernel family serves the four decode entry points of the reference
-// (contiguous MHA/GQA decode, continuous batching, paged decode, INT8 decode):
+// One kernel family serves every decode entry point (contiguous MHA/GQA and
+// sliding-window decode, continuous batching, paged decode, INT8 decode, INT8
+// KV cache):
 //
 //   grid  = B * H_KV * head_groups * splits workgroups of 256 threads (4 waves)
 //   block = one KV head's key range [split*chunk, min(len_b, (split+1)*chunk))
 //           for GB query heads of that KV head's group, so each K/V byte is read
 //           from HBM once per group instead of once per query head.
 //
-// Inside a wave a key row of D fp16 is spread over LPR = DP/8 lanes, each lane
-// holding 16 contiguous bytes, so every dwordx4 load instruction reads
-// 64/LPR whole rows (fully coalesced 128-byte lines).  QK^T is v_dot2_f32_f16
-// over the lane's 8 columns followed by a DPP reduction over the LPR lanes of
-// the row; each group of LPR lanes keeps its own online-softmax state
-// (m, l, acc[8]) for the rows it owns, and the states are merged across lanes
-// and waves only once, at the end of the split.  A sequence covered by one
-// split writes the fp16 output directly; otherwise each split writes a
-// (log2-sum-exp, normalised output) partial, bumps its unit's arrival counter,
-// and the last split to arrive merges the partials -- one kernel per call, no
-// separate combine launch.  The last split also resets the counter, so a
-// zero-filled workspace stays zero-filled between calls (and across graph
-// replays) without any memset.
+// Each wave walks 32-key tiles (16 at D = 256).  QK^T runs on MFMA
+// (v_mfma_f32_16x16x32_f16, or the int8 MFMA for INT8 decode) with the query
+// heads as the 16 M rows and 16 keys as N; K comes straight from HBM in the
+// B-operand layout, or (continuous batching, paged) through a per-wave LDS
+// buffer filled by row-coalesced HBM->LDS copies.  P V runs on the VALU in a
+// row layout: a key row of D fp16 over LPR = DP/8 lanes, 16 contiguous bytes
+// each (every dwordx4 load reads 64/LPR whole rows), two keys per
+// v_dot2_f32_f16.  Every lane of a wave shares the online-softmax max, so the
+// waves' (m, l, O) merge once, at the end of the split, through LDS.  A
+// sequence covered by one split writes the fp16 output directly; otherwise
+// each split writes a (log2-sum-exp, normalised output) partial, takes an
+// arrival rank on its unit's counter, and the last split to arrive merges the
+// partials -- one kernel per call, no separate combine launch.  The last split
+// also resets the counter, so a zero-filled workspace stays zero-filled
+// between calls (and across graph replays) without any memset.
 #include <math.h>
 
 #include <algorithm>
@@ -81,7 +84,7 @@ struct DecodeParams {
   const float* k_scale;        // INT8
   float* ws_o;                 // [B*H_Q, S, DP] normalised partial outputs
   float* ws_lse;               // [B*H_Q, S] log2-sum-exp of each partial
-  unsigned* counters;          // [2 * kCounterSlots] arrivals, then publications, per unit; zero between calls
+  unsigned* counters;          // [kCounterSlots] arrival counters, one per unit; zero between calls
   int unit_base;               // first unit of this launch
   int B, H_Q, H_KV, N, D, G;
   int fixed_len;               // decode / INT8: number of attended keys
