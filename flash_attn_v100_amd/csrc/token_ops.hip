@@ -234,14 +234,19 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(const half_t* __restric
 // partial sum, so each sum is accumulated serially in index order, as there.
 // One workgroup of two waves per batch row: wave 0 computes Z and then the
 // residual sample, wave 1 the bonus token, concurrently.  Within a wave the 64
-// lanes load 256 consecutive elements and compute their terms (differences,
-// the division by Z) in parallel into LDS, with the next 256 already loading;
-// lane 0 then runs only the dependent adds, every lane tests the running sums,
-// and the sample and bonus scans stop at their first decisive hit.
+// lanes load kChunk consecutive elements and compute their terms (differences,
+// the division by Z) in parallel into LDS, with the next chunk already
+// loading; lane 0 then runs only the dependent adds, 64 terms per batch read
+// from LDS, and tests the running sum once per batch: sums only grow, so the
+// first hit lies in the batch where the test first passes, and lane 0 replays
+// that batch's adds one by one (the same adds in the same order, so the same
+// sums) to find it.  The sample and bonus scans stop at their first decisive
+// hit.
 namespace spec {
 
 constexpr int kMaxK = 8;     // SPEC_MAX_K (flash_attn_kernel.cu:3851)
-constexpr int kChunk = 256;  // elements per wave step (4 per lane)
+constexpr int kChunk = 2048;  // elements per wave step (32 per lane)
+constexpr int kPerLane = kChunk / 64;
 
 enum ChainMode { kZ = 0, kResidual = 1, kPrefix = 2, kBonus = 3 };
 
@@ -251,124 +256,119 @@ enum ChainMode { kZ = 0, kResidual = 1, kPrefix = 2, kBonus = 3 };
 //  kPrefix:   cs += a; hit when r < cs.
 //  kBonus:    cs += a; hit when cs >= r.
 // Returns the reference's token: the first hit, or the next hit if the first
-// is index 0 (0 without hits).  Per 256-element chunk: every lane computes 4
-// terms into LDS (a term that does not contribute is -0.0, which leaves a
-// non-negative running sum unchanged, so the chain needs no test); lane 0
-// runs the dependent adds over them, 64 at a time in registers, writing the
-// running sums back; then every lane tests 4 of them and a ballot finds the
-// first hit.  For kResidual the first v with r < cs always contributed (cs
-// only grows where a term is added); a later hit must contribute too.
+// is index 0 (0 without hits).  A term that does not contribute (a - b <= 0
+// for kZ / kResidual, or past V) is -0.0, which leaves a non-negative running
+// sum unchanged; a contributing term has its sign bit clear (+0.0 if the
+// division underflows), so the replay reads "contributed" off the sign.  For
+// kResidual the first v with r < cs always contributed (cs only grows where
+// a term is added); a later hit must contribute too.
 template <int MODE>
 __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, int V, float Z, float r, float* sum,
                      float* lds) {
   const int lane = threadIdx.x & 63;
-  float cs = 0.0f;  // lane 0's running sum
-  int tok = 0;
-  bool zero_hit = false;  // a hit at index 0 was seen: the next hit decides
-  auto load = [&](int c0, float (&x)[4], float (&y)[4]) {
+  float cs = 0.0f;        // lane 0's running sum
+  int tok = 0;            // lane 0: the token found so far
+  bool zero_hit = false;  // lane 0: a hit at index 0 was seen, the next hit decides
+  // lane l holds elements c0 + 256 q + 4 l + e (q < kPerLane / 4, e < 4): 16-byte loads
+  // 16-byte loads where the row allows them (V % 4 == 0 and 16-byte aligned
+  // rows), element loads otherwise
+  const bool vec = (V & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
+                   (MODE == kPrefix || MODE == kBonus || (reinterpret_cast<uintptr_t>(b) & 15) == 0);
+  auto load = [&](int c0, float4_t (&x)[kPerLane / 4], float4_t (&y)[kPerLane / 4]) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int v = c0 + 4 * lane + e;
-      x[e] = v < V ? a[v] : 0.0f;
-      if constexpr (MODE == kZ || MODE == kResidual) y[e] = v < V ? b[v] : 0.0f;
+    for (int q = 0; q < kPerLane / 4; ++q) {
+      const int v0 = c0 + 256 * q + 4 * lane;
+      if (vec) {
+        const bool in = v0 < V;
+        x[q] = in ? *reinterpret_cast<const float4_t*>(a + v0) : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (MODE == kZ || MODE == kResidual)
+          y[q] = in ? *reinterpret_cast<const float4_t*>(b + v0) : float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[q][e] = v0 + e < V ? a[v0 + e] : 0.0f;
+          if constexpr (MODE == kZ || MODE == kResidual) y[q][e] = v0 + e < V ? b[v0 + e] : 0.0f;
+        }
+      }
     }
   };
-  float xa[4], ya[4], xn[4], yn[4];
+  float4_t xn[kPerLane / 4], yn[kPerLane / 4];
   load(0, xn, yn);
   for (int c0 = 0; c0 < V; c0 += kChunk) {
+    float4_t xa[kPerLane / 4], ya[kPerLane / 4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      xa[e] = xn[e];
-      ya[e] = yn[e];
+    for (int q = 0; q < kPerLane / 4; ++q) {
+      xa[q] = xn[q];
+      ya[q] = yn[q];
     }
     if (c0 + kChunk < V) load(c0 + kChunk, xn, yn);
-    bool contrib[4];
-    float4_t t4;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float t;
-      if constexpr (MODE == kZ || MODE == kResidual) {
-        const float d = xa[e] - ya[e];
-        contrib[e] = d > 0.0f;
-        t = contrib[e] ? (MODE == kZ ? d : d / Z) : -0.0f;
-      } else {
-        contrib[e] = true;
-        t = xa[e];
+    for (int q = 0; q < kPerLane / 4; ++q) {
+      float4_t t4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t;
+        if constexpr (MODE == kZ || MODE == kResidual) {
+          const float d = xa[q][e] - ya[q][e];
+          t = d > 0.0f ? (MODE == kZ ? d : d / Z) : -0.0f;
+        } else {
+          t = xa[q][e];
+        }
+        if (c0 + 256 * q + 4 * lane + e >= V) t = -0.0f;  // past V: no change, never a hit
+        t4[e] = t;
       }
-      // elements past V add -0.0 (no change) and never hit
-      if (c0 + 4 * lane + e >= V) {
-        t = -0.0f;
-        contrib[e] = false;
-      }
-      t4[e] = t;
+      *reinterpret_cast<float4_t*>(lds + 256 * q + 4 * lane) = t4;
     }
-    *reinterpret_cast<float4_t*>(lds + 4 * lane) = t4;
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+    bool done = false;
     if (lane == 0) {
-#pragma unroll
-      for (int h = 0; h < kChunk; h += 64) {
+      const int n = min(kChunk, V - c0);
+      for (int h = 0; h < n; h += 64) {
         float4_t q[16];
 #pragma unroll
         for (int j = 0; j < 16; ++j) q[j] = *reinterpret_cast<const float4_t*>(lds + h + 4 * j);
+        const float cs0 = cs;
 #pragma unroll
         for (int j = 0; j < 16; ++j)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            cs += q[j][e];
-            q[j][e] = cs;
+          for (int e = 0; e < 4; ++e) cs += q[j][e];
+        if constexpr (MODE != kZ) {
+          const bool crossed = (MODE == kBonus) ? (cs >= r) : (r < cs);
+          if (crossed || zero_hit) {
+            // replay the batch: the first hit, or the next one after a hit at 0
+            float x = cs0;
+            for (int k = 0; k < 64 && !done; ++k) {
+              const float t = lds[h + k];  // the batch's terms are still staged there
+              x += t;
+              const int v = c0 + h + k;
+              if (v >= V) break;
+              const bool contrib = MODE != kResidual || !__builtin_signbit(t);
+              const bool hit = (MODE == kBonus) ? (x >= r) : (r < x) && contrib;
+              if (!hit) continue;
+              if (v == 0 && !zero_hit) {
+                zero_hit = true;
+              } else {
+                tok = v;
+                done = true;
+              }
+            }
+            if (done) break;
           }
-        if constexpr (MODE != kZ)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) *reinterpret_cast<float4_t*>(lds + h + 4 * j) = q[j];
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);
-    if constexpr (MODE != kZ) {
-      const float4_t c4 = *reinterpret_cast<const float4_t*>(lds + 4 * lane);
-      int best = -1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const bool hit = (MODE == kBonus) ? (c4[e] >= r) : (r < c4[e]) && contrib[e];
-        const int v = c0 + 4 * lane + e;
-        // after a hit at index 0 only later hits (v > 0) count
-        const bool ok = hit && !(v == 0 && zero_hit);
-        if (ok && best < 0) best = v;
-      }
-      // lowest v with a hit across the wave: lanes are ordered, so the first lane with a hit wins
-      const unsigned long long m = __builtin_amdgcn_ballot_w64(best >= 0);
-      if (m != 0) {
-        const int src = __builtin_ctzll(m);
-        const int v0 = __builtin_amdgcn_readlane(best, src);
-        if (v0 != 0) {
-          tok = v0;
-          break;
-        }
-        // the hit is index 0: remember it and look for the next one
-        zero_hit = true;
-        int best2 = -1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = c0 + 4 * lane + e;
-          const bool hit = (MODE == kBonus) ? (c4[e] >= r) : (r < c4[e]) && contrib[e];
-          if (hit && v > 0 && best2 < 0) best2 = v;
-        }
-        const unsigned long long m2 = __builtin_amdgcn_ballot_w64(best2 >= 0);
-        if (m2 != 0) {
-          tok = __builtin_amdgcn_readlane(best2, __builtin_ctzll(m2));
-          break;
         }
       }
     }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lane 0's LDS reads are done before the next chunk's writes
+    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done))) break;
   }
   if (sum) *sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs)));
-  return tok;
+  return __builtin_amdgcn_readfirstlane(tok);
 }
 
 __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ target, const float* __restrict__ draft,
                                                      const int64_t* __restrict__ draft_tokens,
                                                      const float* __restrict__ rand, int32_t* __restrict__ accepted,
                                                      int64_t* __restrict__ out, int K, int V) {
-  __shared__ __attribute__((aligned(16))) float lds[2][kChunk];  // per-wave term / running-sum staging
+  __shared__ __attribute__((aligned(16))) float lds[2][kChunk];  // per-wave term staging
   const int b = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
