@@ -2,7 +2,8 @@
 //
 // Workgroup = 4 waves; each wave owns RW = 32 query rows of one (batch, head),
 // so a workgroup covers 128 rows.  The KV sequence is walked in 32-key tiles
-// that stream through a ring of NS LDS stages (3, or 2 for D > 128).  Each
+// that stream through a ring of NS LDS stages (3 for D <= 64, 2 above; on
+// N(0,1) data two stages ran 5a 2 % faster than three at D = 128).  Each
 // stage holds one K and one V tile, unpadded, with the 16-byte chunks of row r
 // XOR-swizzled by chunk_swizzle(r) so that both LDS read patterns below are
 // free of bank conflicts:
@@ -86,7 +87,7 @@ struct PrefillParams {
 #define FA_PRE_NSW 4
 #endif
 #ifndef FA_PRE_NS128
-#define FA_PRE_NS128 3
+#define FA_PRE_NS128 2
 #endif
 #ifndef FA_PRE_W128
 #define FA_PRE_W128 3
