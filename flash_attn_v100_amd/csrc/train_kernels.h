@@ -32,7 +32,7 @@
 // Tiles stream through LDS.  fp16 tiles use the prefill's XOR-swizzled,
 // unpadded layout (both read patterns above are bank-conflict free); with
 // D = 64 or 128 and aligned rows they are copied HBM -> LDS by
-// global_load_lds (no register staging) through a 3-stage ring, two tiles
+// global_load_lds (no register staging) through a two-stage ring, one tile
 // ahead, one barrier per tile.  fp32 tiles and odd D stage through registers
 // into a two-stage ring (fp32 rows padded by 32 bytes).
 //
@@ -197,9 +197,9 @@ __device__ __forceinline__ typename Elem<T>::frag acc_frag(const float16_t& a, i
 // per-row float vectors) through an LDS ring.  A stage holds
 //   [tensor A tile | tensor B tile | VECS: 64 floats of vector 0 | 64 of vector 1]
 // (only the first 32 floats of each vector slot are used).
-//  DMA (fp16, D = DP, 16-byte aligned rows): NS = 3 stages filled by
-//    global_load_lds; rows past `rows` re-read the last row (callers mask them).
-//  otherwise: NS = 2 stages filled through registers; rows past `rows` are 0
+//  DMA (fp16, D = DP, 16-byte aligned rows): stages filled by global_load_lds,
+//    one tile ahead; rows past `rows` re-read the last row (callers mask them).
+//  otherwise: stages filled through registers; rows past `rows` are 0
 //    and vector 0 / vector 1 read +inf / 0 there.
 // Vector 0 is stored pre-multiplied by log2(e) on the register path only; DMA
 // consumers scale at the read (vec_scale()).
@@ -207,7 +207,7 @@ template <typename T, int DP, bool DMA, bool VECS>
 struct TileRing {
   typedef typename Elem<T>::frag F;
   typedef Layout<T, DP> L;
-  static constexpr int NS = DMA ? 3 : 2;
+  static constexpr int NS = 2;  // three DMA stages measured 4.7 % slower (config 7 backward 367 vs 350 us)
   static constexpr int VEC_FLOATS = VECS ? 128 : 0;
   static constexpr int STAGE_BYTES = 2 * L::TILE * static_cast<int>(sizeof(T)) + VEC_FLOATS * 4;
   static constexpr int BYTES = NS * STAGE_BYTES;
@@ -422,7 +422,7 @@ __device__ __forceinline__ void run_ring(Ring& ring, const T* pa, const T* pb, c
     for (int s = 0; s < NS - 1; ++s)
       if (s < ntiles) ring.dma(pa, pb, va, vb, row_of(s), rows, d, s);
     auto step = [&](int t) {
-      ring.wait_dma(t + 1 < ntiles);  // this wave's copies of tile t landed
+      ring.wait_dma(NS > 2 && t + 1 < ntiles);  // this wave's copies of tile t landed (tile t + 1 may be in flight)
       tile_barrier();                  // everyone's did; stage (t - 1) % NS is free
       if (t + NS - 1 < ntiles) ring.dma(pa, pb, va, vb, row_of(t + NS - 1), rows, d, (t + NS - 1) % NS);
     };
