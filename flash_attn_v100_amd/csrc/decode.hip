@@ -42,7 +42,7 @@ constexpr int kPage = 16;             // PAGE_BLOCK_SIZE of the paged cache
 // Split sizing.  The FA_DEC_* macros exist only to let a tuning sweep build
 // variants; the defaults are the shipped configuration.
 #ifndef FA_DEC_TARGET_BLOCKS
-#define FA_DEC_TARGET_BLOCKS 8192
+#define FA_DEC_TARGET_BLOCKS 4096
 #endif
 #ifndef FA_DEC_CHUNK_QUANTUM
 #define FA_DEC_CHUNK_QUANTUM 256
@@ -54,7 +54,7 @@ constexpr int kTargetBlocks = FA_DEC_TARGET_BLOCKS;    // aim for this many spli
 // The paged kernel stages each split's page ids in LDS before its first load,
 // one extra memory round trip per split, so it prefers fewer, longer splits.
 #ifndef FA_DEC_PAGED_DIV
-#define FA_DEC_PAGED_DIV 8
+#define FA_DEC_PAGED_DIV 4
 #endif
 constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / FA_DEC_PAGED_DIV;
 // Every sequence of a fixed-length call (contiguous / INT8 / sliding-window
