@@ -66,6 +66,7 @@ constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / FA_DEC_PAGED_DIV;
 constexpr int kTargetBlocksFixed = FA_DEC_TARGET_BLOCKS_FIXED;
 constexpr int kFixedQuantum = 256;  // fixed-length split boundaries (kSmallGridQuantum below)
 constexpr int kMaxSplits = 128;
+constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this many units run split-major
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
 struct DecodeParams {
@@ -231,8 +232,17 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   preload_args<MODE>(p);
 
   const int S = p.num_splits;
-  const int split = blockIdx.x % S;
-  const int slot = blockIdx.x / S;  // this launch's counter slot
+  // Workgroup -> (unit slot, split).  Fixed-length launches of many units
+  // deal the splits split-major (workgroup j: split j / units, unit j % units),
+  // so the workgroups resident at any time spread over every unit's first
+  // keys instead of one unit's whole range (sliding-window decode at
+  // B = 16: 28.6 -> 27.7 us); small launches (config 2: 8 units, 9.3 us
+  // split-major against 8.8) keep a unit's splits consecutive.
+  constexpr bool kFixedLen = MODE == kModeDecode || MODE == kModeInt8 || MODE == kModeInt8KV;
+  const int nslots = static_cast<int>(gridDim.x) / S;
+  const bool split_major = kFixedLen && nslots >= kSplitMajorUnits;
+  const int split = split_major ? static_cast<int>(blockIdx.x) / nslots : blockIdx.x % S;
+  const int slot = split_major ? static_cast<int>(blockIdx.x) % nslots : blockIdx.x / S;  // this launch's counter slot
   const int rest = p.unit_base + slot;  // (b, h_kv, head group) unit
   const int hg = rest % p.num_hg;
   const int pair = rest / p.num_hg;
