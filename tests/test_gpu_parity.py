@@ -784,3 +784,28 @@ def test_decode_split_tail_boundaries(fa, n):
     o8 = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), n - 1)
     r8 = A.decode_int8(q, k, v, qs, ks, n - 1)
     assert rel_l2(o8, r8) <= INT8_REL_L2
+
+
+# ---------------------------------------------------------------- many-unit fixed-length launches
+
+@pytest.mark.parametrize("mode", ["decode", "window", "int8_cache"])
+def test_fixed_length_many_units(fa, mode):
+    """B=16 with 8 KV heads: 128 (batch, KV head) units, so fixed-length decode
+    deals its splits split-major (every split index of every unit before the
+    next split index); each mode against the oracle on every output row."""
+    b, hq, hkv, n, d, cl = 16, 32, 8, 1537, 128, 1536
+    g = gen(1600 + len(mode))
+    q = randn(g, b, hq, 1, d)
+    if mode == "int8_cache":
+        k8, v8, ks, vs = _int8_cache(g, b, hkv, n, d)
+        out = fa.forward_decode_int8_kv_cache_gqa(*cuda(q, k8, v8, ks, vs), cl)
+        ref = A.decode_int8_kv_cache(q, k8, v8, ks, vs, cl)
+    else:
+        k, v = randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+        if mode == "decode":
+            out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, cl)
+            ref = A.decode(q, k, v, True, cl)
+        else:
+            out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, cl, 1024, 64)
+            ref = A.decode_sliding_window(q, k, v, cl, 1024, 64)
+    assert_close(out, ref, what=f"{mode} many units")
