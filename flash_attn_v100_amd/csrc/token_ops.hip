@@ -236,7 +236,9 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(const half_t* __restric
 // residual sample, wave 1 the bonus token, concurrently.  Within a wave the 64
 // lanes load kChunk consecutive elements and compute their terms (differences,
 // the division by Z) in parallel into LDS, with the next chunk already
-// loading; lane 0 then runs only the dependent adds, 64 terms per batch read
+// loading -- for Z and the residual only the terms that change the sum,
+// compacted in index order with their indices (config 9: 327 -> 240 us);
+// lane 0 then runs only the dependent adds, 64 terms per batch read
 // from LDS, and tests the running sum once per batch: sums only grow, so the
 // first hit lies in the batch where the test first passes, and lane 0 replays
 // that batch's adds one by one (the same adds in the same order, so the same
@@ -262,9 +264,16 @@ enum ChainMode { kZ = 0, kResidual = 1, kPrefix = 2, kBonus = 3 };
 // division underflows), so the replay reads "contributed" off the sign.  For
 // kResidual the first v with r < cs always contributed (cs only grows where
 // a term is added); a later hit must contribute too.
+//
+// kZ and kResidual stage only the contributing terms, compacted in index
+// order with their indices: a non-contributing term is -0.0 and adding it to
+// the non-negative running sum changes nothing, so lane 0 runs the same adds
+// in the same order over the contributing terms alone (about half of them for
+// unrelated target and draft rows).
 template <int MODE>
 __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, int V, float Z, float r, float* sum,
-                     float* lds) {
+                     float* lds, int* lds_idx) {
+  constexpr bool kCompact = MODE == kZ || MODE == kResidual;
   const int lane = threadIdx.x & 63;
   float cs = 0.0f;        // lane 0's running sum
   int tok = 0;            // lane 0: the token found so far
@@ -302,27 +311,55 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
       ya[q] = yn[q];
     }
     if (c0 + kChunk < V) load(c0 + kChunk, xn, yn);
+    int staged = min(kChunk, V - c0);  // terms lane 0 walks in this chunk
+    if constexpr (kCompact) {
+      int base = 0;
 #pragma unroll
-    for (int q = 0; q < kPerLane / 4; ++q) {
-      float4_t t4;
+      for (int q = 0; q < kPerLane / 4; ++q) {
+        float t[4];
+        bool f[4];
+        uint64_t bal[4];
+        int below = 0, total = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float t;
-        if constexpr (MODE == kZ || MODE == kResidual) {
+        for (int e = 0; e < 4; ++e) {
           const float d = xa[q][e] - ya[q][e];
-          t = d > 0.0f ? (MODE == kZ ? d : d / Z) : -0.0f;
-        } else {
-          t = xa[q][e];
+          f[e] = d > 0.0f && c0 + 256 * q + 4 * lane + e < V;
+          t[e] = MODE == kZ ? d : d / Z;
+          bal[e] = __builtin_amdgcn_ballot_w64(f[e]);
+          below += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[e] >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[e]), 0u));
+          total += __builtin_popcountll(bal[e]);
         }
-        if (c0 + 256 * q + 4 * lane + e >= V) t = -0.0f;  // past V: no change, never a hit
-        t4[e] = t;
+        // element order c0 + 256 q + 4 lane + e: lanes below first, then e
+        int pos = base + below;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (f[e]) {
+            lds[pos] = t[e];
+            lds_idx[pos] = c0 + 256 * q + 4 * lane + e;
+            ++pos;
+          }
+        base += total;
       }
-      *reinterpret_cast<float4_t*>(lds + 256 * q + 4 * lane) = t4;
+      lds[base + lane] = -0.0f;  // pad the last batch of 64: no change, never a hit
+      staged = base;
+    } else {
+#pragma unroll
+      for (int q = 0; q < kPerLane / 4; ++q) {
+        float4_t t4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = xa[q][e];
+          if (c0 + 256 * q + 4 * lane + e >= V) t = -0.0f;  // past V: no change, never a hit
+          t4[e] = t;
+        }
+        *reinterpret_cast<float4_t*>(lds + 256 * q + 4 * lane) = t4;
+      }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
     bool done = false;
     if (lane == 0) {
-      const int n = min(kChunk, V - c0);
+      const int n = staged;
       for (int h = 0; h < n; h += 64) {
         float4_t q[16];
 #pragma unroll
@@ -338,13 +375,13 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
             // replay the batch: the first hit, or the next one after a hit at 0
             float x = cs0;
             for (int k = 0; k < 64 && !done; ++k) {
+              if (h + k >= n) break;
               const float t = lds[h + k];  // the batch's terms are still staged there
               x += t;
-              const int v = c0 + h + k;
-              if (v >= V) break;
               const bool contrib = MODE != kResidual || !__builtin_signbit(t);
               const bool hit = (MODE == kBonus) ? (x >= r) : (r < x) && contrib;
               if (!hit) continue;
+              const int v = kCompact ? lds_idx[h + k] : c0 + h + k;
               if (v == 0 && !zero_hit) {
                 zero_hit = true;
               } else {
@@ -368,7 +405,9 @@ __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ t
                                                      const int64_t* __restrict__ draft_tokens,
                                                      const float* __restrict__ rand, int32_t* __restrict__ accepted,
                                                      int64_t* __restrict__ out, int K, int V) {
-  __shared__ __attribute__((aligned(16))) float lds[2][kChunk];  // per-wave term staging
+  // per-wave term staging, plus one batch of padding past the last staged term
+  __shared__ __attribute__((aligned(16))) float lds[2][kChunk + 64];
+  __shared__ int lds_idx[2][kChunk];                                  // their indices (compacted chains)
   const int b = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -407,15 +446,15 @@ __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ t
       const float* ti = tb + static_cast<size_t>(rej) * V;
       const float* di = db + static_cast<size_t>(rej) * V;
       float Z;
-      chain<kZ>(ti, di, V, 0.0f, 0.0f, &Z, lds[0]);
-      const int s = Z > 0.0f ? chain<kResidual>(ti, di, V, Z, rb[rej], nullptr, lds[0])
-                             : chain<kPrefix>(ti, nullptr, V, 0.0f, rb[rej], nullptr, lds[0]);
+      chain<kZ>(ti, di, V, 0.0f, 0.0f, &Z, lds[0], lds_idx[0]);
+      const int s = Z > 0.0f ? chain<kResidual>(ti, di, V, Z, rb[rej], nullptr, lds[0], lds_idx[0])
+                             : chain<kPrefix>(ti, nullptr, V, 0.0f, rb[rej], nullptr, lds[0], lds_idx[0]);
       if (lane == 0) ob[rej] = s;
     }
   } else {
     const int row = rej >= 0 ? rej + 1 : K;
     const float r = rb[rej >= 0 ? min(rej, K - 1) : K - 1];
-    const int bonus = chain<kBonus>(tb + static_cast<size_t>(row) * V, nullptr, V, 0.0f, r, nullptr, lds[1]);
+    const int bonus = chain<kBonus>(tb + static_cast<size_t>(row) * V, nullptr, V, 0.0f, r, nullptr, lds[1], lds_idx[1]);
     if (lane == 0) ob[row] = bonus;
   }
 }
