@@ -2,6 +2,7 @@
 mask (pure index and copy work), including ties (stable order), num_evict at
 0, N and beyond, N up to the 1024 limit, and D not a multiple of 8."""
 import pytest
+import numpy as np
 import torch
 
 from oracle import attention as A
@@ -135,6 +136,35 @@ def test_speculative_verify_zero_hit_across_chunks(fa):
     _check_spec(fa, tp, dp, tok, rv, 1)
     _, rout = A.speculative_verify(tp, dp, tok, rv, 1)
     assert int(rout[0, 0]) == 1500
+
+
+def test_speculative_verify_residual_at_a_running_sum(fa):
+    """r equal to one of the residual scan's own fp32 running sums, so the
+    sampled index depends on every rounding of the serial sum over the
+    contributing terms (about half of a row, spread over several scan chunks
+    and a ragged tail)."""
+    V = 5003
+    g = torch.Generator().manual_seed(13)
+    tp = torch.softmax(torch.randn(1, 2, V, generator=g), -1)
+    dp = torch.softmax(torch.randn(1, 1, V, generator=g), -1)
+    d = (tp[0, 0] - dp[0, 0]).numpy().astype(np.float32)
+    z = np.float32(0.0)
+    for x in d:
+        if x > 0:
+            z = np.float32(z + x)
+    cs, sums = np.float32(0.0), []
+    for v, x in enumerate(d):
+        if x > 0:
+            cs = np.float32(cs + np.float32(x / z))
+            sums.append((v, cs))
+    ratio = (tp[0, 0] / (dp[0, 0] + 1e-10)).numpy()
+    tok = int(np.argmin(ratio))  # least acceptable draft token: rejected once r >= its ratio
+    j = next(i for i, (_, c) in enumerate(sums) if c > max(0.6, float(ratio[tok])))
+    r = float(sums[j][1])
+    tokt, rv = torch.tensor([[tok]]), torch.tensor([[r]], dtype=torch.float32)
+    _check_spec(fa, tp, dp, tokt, rv, 1)
+    _, rout = A.speculative_verify(tp, dp, tokt, rv, 1)
+    assert int(rout[0, 0]) > sums[j][0]  # the first index whose running sum exceeds r
 
 
 def test_speculative_verify_validation(fa):
