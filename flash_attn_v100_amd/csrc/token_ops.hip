@@ -301,16 +301,13 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
       }
     }
   };
-  float4_t xn[kPerLane / 4], yn[kPerLane / 4];
-  load(0, xn, yn);
+  // xa / ya hold the current chunk: loaded during the previous chunk's
+  // serial adds, consumed by this chunk's term computation, then reloaded
+  // with the next chunk just before this chunk's adds (so no wait for
+  // memory ever falls between a chunk's terms and its adds)
+  float4_t xa[kPerLane / 4], ya[kPerLane / 4];
+  load(0, xa, ya);
   for (int c0 = 0; c0 < V; c0 += kChunk) {
-    float4_t xa[kPerLane / 4], ya[kPerLane / 4];
-#pragma unroll
-    for (int q = 0; q < kPerLane / 4; ++q) {
-      xa[q] = xn[q];
-      ya[q] = yn[q];
-    }
-    if (c0 + kChunk < V) load(c0 + kChunk, xn, yn);
     int staged = min(kChunk, V - c0);  // terms lane 0 walks in this chunk
     if constexpr (kCompact) {
       int base = 0;
@@ -357,6 +354,7 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
+    if (c0 + kChunk < V) load(c0 + kChunk, xa, ya);
     bool done = false;
     if (lane == 0) {
       const int n = staged;
