@@ -232,22 +232,22 @@ __global__ __launch_bounds__(kThreads) void evict_kernel(const half_t* __restric
 // against r (with its "tok == 0" update rule: a hit at index 0 is replaced by
 // the next hit).  The sampled indices depend on the exact fp32 value of every
 // partial sum, so each sum is accumulated serially in index order, as there.
-// One workgroup of two waves per batch row: wave 0 computes Z and then the
-// residual sample, wave 1 the bonus token, concurrently.  Within a wave the 64
-// lanes load kChunk consecutive elements and compute their terms (differences,
-// the division by Z) in parallel into LDS, with the next chunk already
-// loading -- for Z and the residual only the terms that change the sum,
-// compacted in index order with their indices (config 9: 327 -> 240 us);
-// lane 0 then runs only the dependent adds, 64 terms per batch read
-// from LDS, and tests the running sum once per batch: sums only grow, so the
+// Two workgroups of two waves per batch row: one computes Z and then the
+// residual sample, the other the bonus token, concurrently.  In each, wave 1
+// loads kChunk consecutive elements and stages their terms (differences, the
+// division by Z) into LDS -- for Z and the residual only the terms that change
+// the sum, compacted in index order with their indices -- while lane 0 of
+// wave 0 runs only the dependent adds of the previous chunk, 64 terms per
+// batch, and tests the running sum once per batch: sums only grow, so the
 // first hit lies in the batch where the test first passes, and lane 0 replays
 // that batch's adds one by one (the same adds in the same order, so the same
 // sums) to find it.  The sample and bonus scans stop at their first decisive
-// hit.
+// hit.  (Config 9: 327 us with one workgroup per row staging and adding in
+// turn, 240 with the compaction, 130 with staging and adds on separate waves.)
 namespace spec {
 
 constexpr int kMaxK = 8;     // SPEC_MAX_K (flash_attn_kernel.cu:3851)
-constexpr int kChunk = 2048;  // elements per wave step (32 per lane)
+constexpr int kChunk = 2048;  // elements per staged chunk (32 per lane)
 constexpr int kPerLane = kChunk / 64;
 
 enum ChainMode { kZ = 0, kResidual = 1, kPrefix = 2, kBonus = 3 };
@@ -265,20 +265,31 @@ enum ChainMode { kZ = 0, kResidual = 1, kPrefix = 2, kBonus = 3 };
 // kResidual the first v with r < cs always contributed (cs only grows where
 // a term is added); a later hit must contribute too.
 //
-// kZ and kResidual stage only the contributing terms, compacted in index
-// order with their indices: a non-contributing term is -0.0 and adding it to
-// the non-negative running sum changes nothing, so lane 0 runs the same adds
-// in the same order over the contributing terms alone (about half of them for
-// unrelated target and draft rows).
+// Two waves: wave 1 stages the terms of chunk c + 1 into one LDS buffer
+// while lane 0 of wave 0 adds chunk c from the other; one workgroup barrier
+// per chunk hands the buffers over.  kZ and kResidual stage only the
+// contributing terms, compacted in index order with their indices: adding a
+// non-contributing -0.0 to the non-negative running sum changes nothing, so
+// lane 0 runs the same adds in the same order over about half the terms for
+// unrelated target and draft rows.  Every wave runs the same number of
+// barriers: the loop is bounded by the chunk count and its early exit is read
+// from LDS after a barrier.
+struct Stage {
+  float t[2][kChunk + 64];  // terms (+ one batch of -0.0 padding)
+  int idx[2][kChunk];       // their indices (compacted modes)
+  int n[2];                 // terms staged
+  int done, tok;
+  float sum;
+};
+
 template <int MODE>
 __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, int V, float Z, float r, float* sum,
-                     float* lds, int* lds_idx) {
+                     Stage& st) {
   constexpr bool kCompact = MODE == kZ || MODE == kResidual;
   const int lane = threadIdx.x & 63;
-  float cs = 0.0f;        // lane 0's running sum
-  int tok = 0;            // lane 0: the token found so far
-  bool zero_hit = false;  // lane 0: a hit at index 0 was seen, the next hit decides
-  // lane l holds elements c0 + 256 q + 4 l + e (q < kPerLane / 4, e < 4): 16-byte loads
+  const int wave = threadIdx.x >> 6;
+  const int nchunks = (V + kChunk - 1) / kChunk;
+  // lane l holds elements c0 + 256 q + 4 l + e (q < kPerLane / 4, e < 4):
   // 16-byte loads where the row allows them (V % 4 == 0 and 16-byte aligned
   // rows), element loads otherwise
   const bool vec = (V & 3) == 0 && (reinterpret_cast<uintptr_t>(a) & 15) == 0 &&
@@ -301,67 +312,73 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
       }
     }
   };
-  // xa / ya hold the current chunk: loaded during the previous chunk's
-  // serial adds, consumed by this chunk's term computation, then reloaded
-  // with the next chunk just before this chunk's adds (so no wait for
-  // memory ever falls between a chunk's terms and its adds)
-  float4_t xa[kPerLane / 4], ya[kPerLane / 4];
-  load(0, xa, ya);
-  for (int c0 = 0; c0 < V; c0 += kChunk) {
-    int staged = min(kChunk, V - c0);  // terms lane 0 walks in this chunk
+  // wave 1: stage chunk c into buffer c & 1
+  auto stage = [&](int c) {
+    const int c0 = c * kChunk;
+    const int buf = c & 1;
+    float4_t x[kPerLane / 4], y[kPerLane / 4];
+    load(c0, x, y);
+    float* t_out = st.t[buf];
     if constexpr (kCompact) {
       int base = 0;
 #pragma unroll
       for (int q = 0; q < kPerLane / 4; ++q) {
         float t[4];
         bool f[4];
-        uint64_t bal[4];
         int below = 0, total = 0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float d = xa[q][e] - ya[q][e];
+          const float d = x[q][e] - y[q][e];
           f[e] = d > 0.0f && c0 + 256 * q + 4 * lane + e < V;
           t[e] = MODE == kZ ? d : d / Z;
-          bal[e] = __builtin_amdgcn_ballot_w64(f[e]);
-          below += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal[e] >> 32),
-                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal[e]), 0u));
-          total += __builtin_popcountll(bal[e]);
+          const uint64_t bal = __builtin_amdgcn_ballot_w64(f[e]);
+          below += __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u));
+          total += __builtin_popcountll(bal);
         }
         // element order c0 + 256 q + 4 lane + e: lanes below first, then e
         int pos = base + below;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (f[e]) {
-            lds[pos] = t[e];
-            lds_idx[pos] = c0 + 256 * q + 4 * lane + e;
+            t_out[pos] = t[e];
+            st.idx[buf][pos] = c0 + 256 * q + 4 * lane + e;
             ++pos;
           }
         base += total;
       }
-      lds[base + lane] = -0.0f;  // pad the last batch of 64: no change, never a hit
-      staged = base;
+      t_out[base + lane] = -0.0f;  // pad the last batch of 64: no change, never a hit
+      if (lane == 0) st.n[buf] = base;
     } else {
 #pragma unroll
       for (int q = 0; q < kPerLane / 4; ++q) {
         float4_t t4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float t = xa[q][e];
-          if (c0 + 256 * q + 4 * lane + e >= V) t = -0.0f;  // past V: no change, never a hit
-          t4[e] = t;
-        }
-        *reinterpret_cast<float4_t*>(lds + 256 * q + 4 * lane) = t4;
+        for (int e = 0; e < 4; ++e) t4[e] = c0 + 256 * q + 4 * lane + e < V ? x[q][e] : -0.0f;  // past V: never a hit
+        *reinterpret_cast<float4_t*>(t_out + 256 * q + 4 * lane) = t4;
       }
+      if (lane == 0) st.n[buf] = min(kChunk, V - c0);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the wave's LDS writes are done
-    if (c0 + kChunk < V) load(c0 + kChunk, xa, ya);
-    bool done = false;
-    if (lane == 0) {
-      const int n = staged;
-      for (int h = 0; h < n; h += 64) {
+  };
+
+  if (threadIdx.x == 0) st.done = 0;
+  if (wave == 1) stage(0);
+  __syncthreads();
+  float cs = 0.0f;        // lane 0 of wave 0: the running sum
+  int tok = 0;            // lane 0 of wave 0: the token found so far
+  bool zero_hit = false;  // lane 0 of wave 0: a hit at index 0 was seen, the next hit decides
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1;
+    if (wave == 1) {
+      if (c + 1 < nchunks) stage(c + 1);
+    } else if (lane == 0) {
+      const float* tb = st.t[buf];
+      const int n = st.n[buf];
+      bool done = false;
+      for (int h = 0; h < n && !done; h += 64) {
         float4_t q[16];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) q[j] = *reinterpret_cast<const float4_t*>(lds + h + 4 * j);
+        for (int j = 0; j < 16; ++j) q[j] = *reinterpret_cast<const float4_t*>(tb + h + 4 * j);
         const float cs0 = cs;
 #pragma unroll
         for (int j = 0; j < 16; ++j)
@@ -374,12 +391,12 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
             float x = cs0;
             for (int k = 0; k < 64 && !done; ++k) {
               if (h + k >= n) break;
-              const float t = lds[h + k];  // the batch's terms are still staged there
+              const float t = tb[h + k];
               x += t;
               const bool contrib = MODE != kResidual || !__builtin_signbit(t);
               const bool hit = (MODE == kBonus) ? (x >= r) : (r < x) && contrib;
               if (!hit) continue;
-              const int v = kCompact ? lds_idx[h + k] : c0 + h + k;
+              const int v = kCompact ? st.idx[buf][h + k] : c * kChunk + h + k;
               if (v == 0 && !zero_hit) {
                 zero_hit = true;
               } else {
@@ -387,35 +404,43 @@ __device__ int chain(const float* __restrict__ a, const float* __restrict__ b, i
                 done = true;
               }
             }
-            if (done) break;
           }
         }
       }
+      if (done) st.done = 1;
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lane 0's LDS reads are done before the next chunk's writes
-    if (__builtin_amdgcn_readfirstlane(static_cast<int>(done))) break;
+    __syncthreads();  // chunk c consumed, chunk c + 1 staged
+    if (st.done) break;
   }
-  if (sum) *sum = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cs)));
-  return __builtin_amdgcn_readfirstlane(tok);
+  if (threadIdx.x == 0) {
+    st.tok = tok;
+    st.sum = cs;
+  }
+  __syncthreads();
+  const int result = st.tok;
+  if (sum) *sum = st.sum;
+  __syncthreads();  // every thread has read tok / sum before the next chain resets them
+  return result;
 }
 
+// Grid (B, 2): workgroup (b, 0) settles the acceptance steps of row b and,
+// after a rejection, samples the residual (Z, then the residual scan);
+// workgroup (b, 1) draws the bonus token.  Both run the (cheap) acceptance
+// steps themselves.
 __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ target, const float* __restrict__ draft,
                                                      const int64_t* __restrict__ draft_tokens,
                                                      const float* __restrict__ rand, int32_t* __restrict__ accepted,
                                                      int64_t* __restrict__ out, int K, int V) {
-  // per-wave term staging, plus one batch of padding past the last staged term
-  __shared__ __attribute__((aligned(16))) float lds[2][kChunk + 64];
-  __shared__ int lds_idx[2][kChunk];                                  // their indices (compacted chains)
+  __shared__ __attribute__((aligned(16))) Stage st;
   const int b = blockIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int role = blockIdx.y;
   const float* tb = target + static_cast<size_t>(b) * (K + 1) * V;
   const float* db = draft + static_cast<size_t>(b) * K * V;
   const int64_t* tok_b = draft_tokens + static_cast<size_t>(b) * K;
   const float* rb = rand + static_cast<size_t>(b) * K;
   int64_t* ob = out + static_cast<size_t>(b) * (K + 1);
 
-  // acceptance steps (wave-uniform: every lane reads the same values)
+  // acceptance steps (uniform: every thread reads the same values)
   int acc = 0;
   int rej = -1;
   for (int i = 0; i < K; ++i) {
@@ -431,10 +456,10 @@ __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ t
       break;
     }
   }
-  if (wave == 0) {
-    if (lane == 0) {
+  if (role == 0) {
+    if (threadIdx.x == 0) {
       // every position is written: accepted tokens, then (after a rejection at
-      // rej) the sample at rej, the bonus at rej + 1 (wave 1) and -1 beyond
+      // rej) the sample at rej, the bonus at rej + 1 (workgroup (b, 1)) and -1 beyond
       for (int i = 0; i < acc; ++i) ob[i] = tok_b[i];
       if (rej >= 0)
         for (int j = rej + 2; j <= K; ++j) ob[j] = -1;
@@ -444,16 +469,16 @@ __global__ __launch_bounds__(128) void verify_kernel(const float* __restrict__ t
       const float* ti = tb + static_cast<size_t>(rej) * V;
       const float* di = db + static_cast<size_t>(rej) * V;
       float Z;
-      chain<kZ>(ti, di, V, 0.0f, 0.0f, &Z, lds[0], lds_idx[0]);
-      const int s = Z > 0.0f ? chain<kResidual>(ti, di, V, Z, rb[rej], nullptr, lds[0], lds_idx[0])
-                             : chain<kPrefix>(ti, nullptr, V, 0.0f, rb[rej], nullptr, lds[0], lds_idx[0]);
-      if (lane == 0) ob[rej] = s;
+      chain<kZ>(ti, di, V, 0.0f, 0.0f, &Z, st);
+      const int s = Z > 0.0f ? chain<kResidual>(ti, di, V, Z, rb[rej], nullptr, st)
+                             : chain<kPrefix>(ti, nullptr, V, 0.0f, rb[rej], nullptr, st);
+      if (threadIdx.x == 0) ob[rej] = s;
     }
   } else {
     const int row = rej >= 0 ? rej + 1 : K;
     const float r = rb[rej >= 0 ? min(rej, K - 1) : K - 1];
-    const int bonus = chain<kBonus>(tb + static_cast<size_t>(row) * V, nullptr, V, 0.0f, r, nullptr, lds[1], lds_idx[1]);
-    if (lane == 0) ob[row] = bonus;
+    const int bonus = chain<kBonus>(tb + static_cast<size_t>(row) * V, nullptr, V, 0.0f, r, nullptr, st);
+    if (threadIdx.x == 0) ob[row] = bonus;
   }
 }
 
@@ -497,7 +522,7 @@ extern "C" int fa_speculative_verify(const float* target_probs, const float* dra
   if (B == 0) return FA_OK;
   if (!target_probs || !draft_probs || !draft_tokens || !random_vals || !accepted_count || !output_tokens)
     return set_error(FA_ERR_INVALID_ARG, "%s: null pointer", fn);
-  hipLaunchKernelGGL(spec::verify_kernel, dim3(B), dim3(128), 0, static_cast<hipStream_t>(stream), target_probs,
+  hipLaunchKernelGGL(spec::verify_kernel, dim3(B, 2), dim3(128), 0, static_cast<hipStream_t>(stream), target_probs,
                      draft_probs, draft_tokens, random_vals, accepted_count, output_tokens, K, vocab_size);
   return check_launch(fn);
 }
