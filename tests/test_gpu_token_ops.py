@@ -93,6 +93,10 @@ def _check_spec(fa, tp, dp, tok, rv, K):
     (42, 4, 5, 128, True, True),      # :160-196 all accepted
     (7, 2, 3, 32000, False, False),   # :240- large vocabulary
     (3, 16, 8, 1000, False, False), (4, 3, 1, 257, False, False), (5, 8, 4, 4099, False, False),
+    (6, 4, 2, 1, False, False),       # one-word vocabulary
+    (8, 4, 3, 63, False, False),      # less than one 64-term batch
+    (9, 6, 2, 2049, False, False),    # one element into a second staged chunk
+    (10, 3, 2, 4096, False, False),   # exactly two chunks
 ])
 def test_speculative_verify(fa, seed, B, K, V, same, zero_rand):
     _check_spec(fa, *_spec(seed, B, K, V, same, zero_rand), K)
