@@ -16,6 +16,9 @@ pytestmark = pytest.mark.gpu
     (3, 2, 255, 128, 100, False), (2, 2, 256, 64, 256, False), (2, 4, 1000, 128, 250, True),
     (1, 8, 1024, 128, 512, False), (2, 2, 300, 36, 77, True), (2, 2, 64, 128, -5, False),
     (1, 2, 50, 128, 80, True),
+    (16, 8, 1024, 128, 256, False),  # 512 output rows per workgroup (the bench shape)
+    (8, 8, 1024, 128, 300, True),    # 256 rows per workgroup
+    (16, 16, 700, 64, 123, True),    # 512 rows per workgroup, ragged last block
 ])
 def test_token_eviction(fa, b, h, n, d, num_evict, ties):
     g = torch.Generator().manual_seed(n + d + num_evict)
