@@ -91,7 +91,7 @@ struct DecodeParams {
   int fixed_len;               // decode / INT8: number of attended keys
   int chunk, num_splits, num_hg;
   int max_num_blocks, num_pages;
-  int lpt;                     // CB / paged: serve sequences longest first
+  int lpt;                     // paged: serve sequences longest first
   int absorb_tail;             // fixed-length: the last split runs to fixed_len
   int seg1, seg_shift;         // contiguous modes: key v < seg1 is row v, later keys row v + seg_shift
                                // (seg_shift = 0: identity; sliding window: sink run, then window run)
@@ -116,7 +116,7 @@ __device__ __forceinline__ void preload_args(const DecodeParams& p) {
   }
   if constexpr (MODE == kModeInt8) asm volatile("" ::"s"(p.q_scale), "s"(p.k_scale), "s"(p.fixed_len), "s"(p.scale));
   if constexpr (MODE == kModeDecode) asm volatile("" ::"s"(p.fixed_len), "s"(p.seg1), "s"(p.seg_shift));
-  if constexpr (MODE == kModeCB) asm volatile("" ::"s"(p.lens), "s"(p.lpt), "s"(p.seg1), "s"(p.seg_shift));
+  if constexpr (MODE == kModeCB) asm volatile("" ::"s"(p.lens), "s"(p.seg1), "s"(p.seg_shift));
   if constexpr (MODE == kModePaged)
     asm volatile("" ::"s"(p.lens), "s"(p.lpt), "s"(p.block_table), "s"(p.bt_numel), "s"(p.max_num_blocks),
                  "s"(p.num_pages));
@@ -253,11 +253,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   const int g_valid = min(GB, G - g_base);  // heads of this group that exist
 
   const int tid = threadIdx.x;
-  // Sequence served.  With per-sequence lengths (lpt set), unit rank r serves
+  // Sequence served.  Paged decode with lpt set: unit rank r serves
   // the sequence of rank r in descending length order (ties by index), so the
   // longest sequences are dispatched first and the short ones fill the tail.
   int b = pair / p.H_KV;
-  if constexpr (MODE == kModeCB || MODE == kModePaged) {
+  if constexpr (MODE == kModePaged) {
     if (p.lpt) {
       __shared__ int s_len[kLptMaxSeqs];
       __shared__ int s_seq;
@@ -1095,7 +1095,13 @@ static int run_decode(const char* fn, DecodeParams p, int max_len, void* ws, siz
   if (pl.splits > kMaxSplits)
     return set_error(FA_ERR_UNSUPPORTED, "%s: %d keys per sequence exceed %d", fn, max_len, kMaxSplits * kMaxChunk);
   p.G = p.H_Q / p.H_KV;
-  p.lpt = (MODE == kModeCB || MODE == kModePaged) && p.B > 1 && p.B <= kLptMaxSeqs;
+  // Longest first for paged decode only: its splits are long (a quarter of
+  // the continuous-batching target), so a long sequence dispatched late
+  // would trail the grid (config 4: 178 us with the order, 194 without).
+  // Continuous batching splits finely enough that no workgroup trails by
+  // much, and skipping the order's per-workgroup length ranking is faster
+  // there (config 3: 184.7 us without, 187.4 with).
+  p.lpt = MODE == kModePaged && p.B > 1 && p.B <= kLptMaxSeqs;
   p.chunk = pl.chunk;
   p.num_splits = pl.splits;
   p.num_hg = pl.num_hg;
