@@ -36,7 +36,7 @@ sys.path.insert(0, REPO)
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 MFMA_FP16_PEAK_TFS = 2500.0  # MI355X dense fp16 MFMA
 MFMA_FP32_PEAK_TFS = 157.3   # MI355X dense fp32 MFMA
-HEADLINE_KERNEL = "decode_splitkv_kernel<128, 4, 0, true>"
+HEADLINE_KERNEL = "decode_splitkv_kernel<128, 4, 0, true, false>"
 
 
 def log(*a):

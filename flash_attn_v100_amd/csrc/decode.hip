@@ -12,8 +12,9 @@
 // Each wave walks 32-key tiles (16 at D = 256).  QK^T runs on MFMA
 // (v_mfma_f32_16x16x32_f16, or the int8 MFMA for INT8 decode) with the query
 // heads as the 16 M rows and 16 keys as N; K comes straight from HBM in the
-// B-operand layout, or (continuous batching, paged) through a per-wave LDS
-// buffer filled by row-coalesced HBM->LDS copies.  P V runs on the VALU in a
+// B-operand layout, or (continuous batching, paged, contiguous decode launches
+// of 512+ workgroups) through a per-wave LDS buffer filled by row-coalesced
+// HBM->LDS copies.  P V runs on the VALU in a
 // row layout: a key row of D fp16 over LPR = DP/8 lanes, 16 contiguous bytes
 // each (every dwordx4 load reads 64/LPR whole rows), two keys per
 // v_dot2_f32_f16.  Every lane of a wave shares the online-softmax max, so the
@@ -214,7 +215,7 @@ __device__ __forceinline__ int counter_index(int slot) {
   return (slot % kLines) * 32 + slot / kLines;
 }
 
-template <int DP, int GB, int MODE, bool VEC>
+template <int DP, int GB, int MODE, bool VEC, bool LDSK>
 // Three waves per SIMD (a 168-register budget): every mode's tile loop fits
 // it without spilling, and the compiler's own choice for the INT8 KV cache
 // (128 registers and a spill, for four waves) measured 14 % slower.
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // (physical chunk = logical ^ (row % 16)) by the choice of source chunk per
   // lane, so the MFMA-layout reads (16 lanes = 16 rows at one chunk) hit 16
   // distinct bank groups.  Each wave owns its tile: no barriers.
-  constexpr bool kLdsK = (MODE == kModeCB || MODE == kModePaged) && VEC;
+  constexpr bool kLdsK = (MODE == kModeCB || MODE == kModePaged || LDSK) && VEC;
   // Every fp16 cache is read once per call: nontemporal loads (measured 11 %
   // faster on the paged cache, 2-3 % on contiguous and INT8 decode; the int8
   // cache's 8-byte V loads measured 8 % slower with them).
@@ -1019,9 +1020,22 @@ static WorkspaceLayout plan_layout(const DecodePlan& pl, int B, int H_Q, int H_K
   return w;
 }
 
+// Contiguous decode stages K in LDS (as continuous batching and paged
+// decode do) when the launch has at least this many workgroups: row-coalesced
+// copies pay off once the call is bandwidth-bound (sliding window at B = 16,
+// 512 workgroups: 27.9 -> 26.7 us) but not for latency-bound small grids
+// (config 2, 256 workgroups: 9.0 -> 9.2 us).
+constexpr int kLdsKMinBlocks = 512;
+
 template <int DP, int GB, int MODE, bool VEC>
 static void launch_split(const DecodeParams& p, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((decode_splitkv_kernel<DP, GB, MODE, VEC>), dim3(blocks), dim3(kDecThreads), 0, st, p);
+  if constexpr (MODE == kModeDecode && VEC) {
+    if (blocks >= kLdsKMinBlocks) {
+      hipLaunchKernelGGL((decode_splitkv_kernel<DP, GB, MODE, VEC, true>), dim3(blocks), dim3(kDecThreads), 0, st, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((decode_splitkv_kernel<DP, GB, MODE, VEC, false>), dim3(blocks), dim3(kDecThreads), 0, st, p);
 }
 
 template <int DP, int MODE, bool VEC>
