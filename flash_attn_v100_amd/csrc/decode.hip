@@ -12,9 +12,9 @@
 // Each wave walks 32-key tiles (16 at D = 256).  QK^T runs on MFMA
 // (v_mfma_f32_16x16x32_f16, or the int8 MFMA for INT8 decode) with the query
 // heads as the 16 M rows and 16 keys as N; K comes straight from HBM in the
-// B-operand layout, or (continuous batching, paged, contiguous decode launches
-// of 512+ workgroups) through a per-wave LDS buffer filled by row-coalesced
-// HBM->LDS copies.  P V runs on the VALU in a
+// B-operand layout, or (continuous batching, paged, contiguous and INT8
+// decode launches of 512+ workgroups) through a per-wave LDS buffer filled by
+// row-coalesced HBM->LDS copies.  P V runs on the VALU in a
 // row layout: a key row of D fp16 over LPR = DP/8 lanes, 16 contiguous bytes
 // each (every dwordx4 load reads 64/LPR whole rows), two keys per
 // v_dot2_f32_f16.  Every lane of a wave shares the online-softmax max, so the
@@ -555,11 +555,19 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
       if constexpr (MODE == kModeInt8) {
         typedef int int4v __attribute__((ext_vector_type(4)));
         int4v ci = {0, 0, 0, 0};
+        if constexpr (kLdsK) {
+          if (tt == 0) wait_vm<UV>();
+        }
 #pragma unroll
         for (int c = 0; c < NC; c += 2) {
           int k0lo, k0hi, k1lo, k1hi;
-          quant8(T.k[tt][c], inv_ks, k0lo, k0hi);
-          quant8(T.k[tt][c + 1], inv_ks, k1lo, k1hi);
+          if constexpr (kLdsK) {
+            quant8(__builtin_bit_cast(u32x4, k_frag(tt, c)), inv_ks, k0lo, k0hi);
+            quant8(__builtin_bit_cast(u32x4, k_frag(tt, c + 1)), inv_ks, k1lo, k1hi);
+          } else {
+            quant8(T.k[tt][c], inv_ks, k0lo, k0hi);
+            quant8(T.k[tt][c + 1], inv_ks, k1lo, k1hi);
+          }
           const int4v av = {qi8[c][0], qi8[c][1], qi8[c + 1][0], qi8[c + 1][1]};
           const int4v bv = {k0lo, k0hi, k1lo, k1hi};
           ci = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, ci, 0, 0, 0);
@@ -1020,16 +1028,17 @@ static WorkspaceLayout plan_layout(const DecodePlan& pl, int B, int H_Q, int H_K
   return w;
 }
 
-// Contiguous decode stages K in LDS (as continuous batching and paged
-// decode do) when the launch has at least this many workgroups: row-coalesced
-// copies pay off once the call is bandwidth-bound (sliding window at B = 16,
-// 512 workgroups: 27.9 -> 26.7 us) but not for latency-bound small grids
-// (config 2, 256 workgroups: 9.0 -> 9.2 us).
+// Contiguous and INT8 decode stage K in LDS (as continuous batching and
+// paged decode do) when the launch has at least this many workgroups:
+// row-coalesced copies pay off once the call is bandwidth-bound (sliding
+// window at B = 16, 512 workgroups: 27.9 -> 26.7 us; INT8 at B = 16:
+// 29.25 -> 29.0 us, its K quantized from the LDS fragments) but not for
+// latency-bound small grids (config 2, 256 workgroups: 9.0 -> 9.2 us).
 constexpr int kLdsKMinBlocks = 512;
 
 template <int DP, int GB, int MODE, bool VEC>
 static void launch_split(const DecodeParams& p, int blocks, hipStream_t st) {
-  if constexpr (MODE == kModeDecode && VEC) {
+  if constexpr ((MODE == kModeDecode || MODE == kModeInt8) && VEC) {
     if (blocks >= kLdsKMinBlocks) {
       hipLaunchKernelGGL((decode_splitkv_kernel<DP, GB, MODE, VEC, true>), dim3(blocks), dim3(kDecThreads), 0, st, p);
       return;
