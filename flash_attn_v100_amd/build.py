@@ -66,13 +66,19 @@ def ext_path() -> str:
 
 
 def build_library(verbose: bool = True) -> str:
-    """Compile the HIP kernels and the C ABI into libflash_attn_mi355x.so."""
+    """Compile the HIP kernels and the C ABI into libflash_attn_mi355x.so.
+
+    ``FA_EXTRA_HIPFLAGS`` (environment, space-separated) is appended to every
+    kernel compile: it is how measurement builds switch on the tuning and
+    ablation macros the kernel sources document (e.g. ``-DFA_ABL_NOCOPY``).
+    The shipped build leaves it unset."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     objs = []
     jobs = []
+    extra = os.environ.get("FA_EXTRA_HIPFLAGS", "").split()
     for src in KERNEL_SOURCES + HOST_SOURCES:
         obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-        cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-I", os.path.join(REPO_DIR, "include")]
+        cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-I", os.path.join(REPO_DIR, "include")]
         if src.endswith(".cpp"):
             cmd += ["-x", "hip"]
         cmd += ["-c", os.path.join(CSRC, src), "-o", obj]

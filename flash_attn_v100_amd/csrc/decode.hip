@@ -712,7 +712,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
       // arithmetic (left to itself the scheduler put the first QK^T MFMA, and
       // its wait for Q and the first K rows, ahead of the V loads; config 2
       // 9.2 -> 9.05 us).  The INT8 modes measured slower with it (5b +4 %).
-      if constexpr (MODE == kModeDecode) __builtin_amdgcn_sched_barrier(0);
+      // With K staged in LDS the barrier is also what the copies' wait relies
+      // on: compute_tile's vmcnt(UV) counts exactly the UV V loads issued after
+      // the K copies, so no other vector-memory load may be scheduled between
+      // the copies and that wait.
+      if constexpr (MODE == kModeDecode || kLdsK) __builtin_amdgcn_sched_barrier(0);
       compute_tile(A, t0);
     }
   };

@@ -74,6 +74,14 @@ struct PrefillParams {
 
 // Tile shape per padded head dim.  The FA_PRE_* macros are tuning hooks for
 // building variants; the defaults are the shipped configuration.
+//
+// Ablation hooks (FA_ABL_*, off by default) remove one part of the tile loop
+// so that a timed run shows what that part costs; such a build computes wrong
+// results and is only ever timed:
+//   FA_ABL_NOCOPY   no tile copies after the first NS - 1 (the waits return at once)
+//   FA_ABL_HOTCOPY  every copy reads the sequence's first tile (always cache-resident)
+//   FA_ABL_NOQK     no QK^T MFMAs (and no K fragment reads)
+//   FA_ABL_NOPV     no P V MFMAs
 #ifndef FA_PRE_RB64
 #define FA_PRE_RB64 1
 #endif
@@ -273,7 +281,14 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE, KSPLIT>::WAVES_PER_SIM
     cp_off[i] = static_cast<unsigned>((cp_row[i] * stride + cp_col[i]) * sizeof(half_t));
   }
   auto issue = [&](int t) {
+#ifdef FA_ABL_NOCOPY
+    if (t >= NS - 1) return;
+#endif
+#ifdef FA_ABL_HOTCOPY
+    const int kt = 0;
+#else
     const int kt = t * kBK;
+#endif
     const unsigned sk = lds_base + (t % NS) * kStageBytes;
     const half_t* kb = kp + static_cast<size_t>(kt) * stride;
     const half_t* vb = vp + static_cast<size_t>(kt) * stride;
@@ -340,12 +355,10 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE, KSPLIT>::WAVES_PER_SIM
   const unsigned v_lane =
       (v_row * DP + (((2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1)) ^ v_sw) * 8) + (s16 & 1) * 4) * sizeof(half_t);
 
-  auto compute_tile = [&](const int t, const bool masked) {
-    const int kt = t * kBK + kw;  // first key of the wave's keys in this tile
+  using STile = float16_t[NBLK][RB];
+  // ---- S^T = K Q^T of tile t ----
+  auto qk_tile = [&](const int t, STile& sacc) {
     const unsigned kaddr = lds_base + (t % NS) * kStageBytes + k_lane + kw * DP * 2;
-    const unsigned vaddr = lds_base + (t % NS) * kStageBytes + kTileBytes + v_lane + kw * DP * 2;
-    // ---- S^T = K Q^T ----
-    float16_t sacc[NBLK][RB];
 #pragma unroll
     for (int blk = 0; blk < NBLK; ++blk)
 #pragma unroll
@@ -358,10 +371,20 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE, KSPLIT>::WAVES_PER_SIM
       for (int blk = 0; blk < NBLK; ++blk) {
         const half8_t a = *lds_at<half8_t>((kaddr ^ (32 * kk)) + blk * 32 * DP * 2);
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb) {
+#ifdef FA_ABL_NOQK
+          if (kk == 0) sacc[blk][rb][0] += static_cast<float>(a[0]);
+#else
           sacc[blk][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[rb][kk], sacc[blk][rb], 0, 0, 0);
+#endif
+        }
       }
     }
+  };
+  // ---- softmax and O^T += V^T P^T of tile t ----
+  auto softmax_pv = [&](const int t, STile& sacc, const bool masked) {
+    const int kt = t * kBK + kw;  // first key of the wave's keys in this tile
+    const unsigned vaddr = lds_base + (t % NS) * kStageBytes + kTileBytes + v_lane + kw * DP * 2;
     // ---- softmax (lane owns query row wq0 + 32 rb + l32) ----
     half8_t pf[RB][2 * NBLK];
 #pragma unroll
@@ -434,10 +457,20 @@ __attribute__((amdgpu_waves_per_eu(PrefillShape<DP, WIDE, KSPLIT>::WAVES_PER_SIM
         }
         const half8_t a = __builtin_shufflevector(part[0], part[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb) {
+#ifdef FA_ABL_NOPV
+          oacc[db][rb][i] += static_cast<float>(a[0]) + static_cast<float>(pf[rb][i][0]);
+#else
           oacc[db][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[rb][i], oacc[db][rb], 0, 0, 0);
+#endif
+        }
       }
     }
+  };
+  auto compute_tile = [&](const int t, const bool masked) {
+    STile sacc;
+    qk_tile(t, sacc);
+    softmax_pv(t, sacc, masked);
   };
 
   for (int t = 0; t < ntiles; ++t) {

@@ -232,10 +232,14 @@ def quantize_int8(x_f16: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
     """``int8 = clamp(roundf(x / s), -127, 127)`` (flash_attn_kernel.cu:2837, :2856).
 
     The division is evaluated as ``x * (1/s)`` in float32 with ``1/s`` correctly
-    rounded: that is the reciprocal-multiply the reference's ``--use_fast_math``
-    build (setup.py:25) turns the division into, and it is what the HIP kernel
-    computes, so the integers agree exactly.  Clamping uses fmin/fmax semantics
-    (a NaN quotient becomes +127, as ``fmaxf(-127, fminf(127, NaN))`` does).
+    rounded.  That is this oracle's choice, shared with the HIP kernel, so the
+    two produce identical integer codes.  The reference divides under
+    ``--use_fast_math`` (setup.py:25), whose exact rounding of ``x / s`` is not
+    known here: a quotient that lands within one ulp of a rounding tie (k + 0.5)
+    may round to the neighbouring code in the reference, so INT8 codes at ties
+    are parity-unpinned against the reference (the rel-L2 tolerance covers the
+    effect on the output).  Clamping uses fmin/fmax semantics (a NaN quotient
+    becomes +127, as ``fmaxf(-127, fminf(127, NaN))`` does).
     """
     inv = (torch.ones_like(s, dtype=torch.float32) / s.to(torch.float32))
     y = x_f16.to(torch.float32) * inv

@@ -292,10 +292,9 @@ def _sample_check_decode_like(out, ref_fn, rows):
         assert_close(out[b:b + 1], ref_fn(b), what=f"row {b}")
 
 
-def test_continuous_batching_config3_sampled(fa):
+def test_continuous_batching_config3_full(fa):
     """BASELINE config 3 at full size (B=64, 32:8 heads, max_N=8193, D=128), cache_lens
-    U[16,8192]; every 2nd sequence, the longest and the shortest are checked against the
-    oracle on that sequence."""
+    U[16,8192]; every sequence is checked against the oracle on that sequence."""
     g = gen(3)
     B, HQ, HKV, MAXN, D = 64, 32, 8, 8193, 128
     cl = torch.randint(16, 8193, (B,), generator=g, dtype=torch.int32)
@@ -304,9 +303,7 @@ def test_continuous_batching_config3_sampled(fa):
     k = torch.randn(B, HKV, MAXN, D, generator=gg, device=DEV).half()
     v = torch.randn(B, HKV, MAXN, D, generator=gg, device=DEV).half()
     out = fa.forward_continuous_batching_fp16(q, k, v, cl.to(DEV), True).cpu()
-    # every 2nd sequence plus the longest and the shortest (longest-first dispatch reorders the work)
-    rows = sorted(set(range(0, B, 2)) | {int(cl.argmax()), int(cl.argmin())})
-    for b in rows:
+    for b in range(B):
         n = min(int(cl[b]) + 1, MAXN)
         ref = A.decode(q[b:b + 1].cpu(), k[b:b + 1, :, :n].cpu(), v[b:b + 1, :, :n].cpu(), True, n - 1)
         assert_close(out[b:b + 1], ref, what=f"cfg3 b={b}")
@@ -387,9 +384,12 @@ def test_paged_decode_empty_sequence_is_nan(fa):
     assert_close(out, A.paged_decode(q, kc, vc, bt, slt, 2), what="paged nan")
 
 
-def test_paged_decode_config4_sampled(fa):
+def test_paged_decode_config4_full(fa):
     """BASELINE config 4 at full size: B=128, 32:8 heads, D=128, 65536 pages,
-    seq_lens U[64,4096], block_table = first 32768 entries of randperm(65536)."""
+    seq_lens U[64,4096], block_table = first 32768 entries of randperm(65536).
+    Every sequence is checked against the oracle's paged formula
+    (A.paged_decode) on the real block_table and the whole host copy of the
+    caches, 16 sequences per oracle call."""
     g = gen(4)
     B, HQ, HKV, D, P, MNB = 128, 32, 8, 128, 65536, 256
     sl = torch.randint(64, 4097, (B,), generator=g, dtype=torch.int32)
@@ -399,13 +399,14 @@ def test_paged_decode_config4_sampled(fa):
     kc = torch.randn(P, HKV, 16, D, generator=gg, device=DEV).half()
     vc = torch.randn(P, HKV, 16, D, generator=gg, device=DEV).half()
     out = fa.forward_paged_decode_gqa_fp16(q, kc, vc, bt.to(DEV), sl.to(DEV), MNB).cpu()
-    # every 4th sequence plus the longest and the shortest
-    for b in sorted(set(range(0, B, 4)) | {int(sl.argmax()), int(sl.argmin())}):
-        n = int(sl[b])
-        pages = bt[b, : (n + 15) // 16].long().to(DEV)
-        kk = kc[pages].permute(1, 0, 2, 3).reshape(1, HKV, -1, D)[:, :, :n].cpu()
-        vv = vc[pages].permute(1, 0, 2, 3).reshape(1, HKV, -1, D)[:, :, :n].cpu()
-        assert_close(out[b:b + 1], A.decode(q[b:b + 1].cpu(), kk, vv, False, 0), what=f"cfg4 b={b}")
+    qh, kh, vh = q.cpu(), kc.cpu(), vc.cpu()
+    del kc, vc
+    for b0 in range(0, B, 16):
+        # rows b0.. of the flat table: the oracle reads entry b * MNB + t / 16 of the
+        # sub-table exactly as the kernel reads entry (b0 + b) * MNB + t / 16 of the whole
+        ref = A.paged_decode(qh[b0:b0 + 16], kh, vh, bt[b0:b0 + 16], sl[b0:b0 + 16], MNB)
+        for b in range(16):
+            assert_close(out[b0 + b:b0 + b + 1], ref[b:b + 1], what=f"cfg4 b={b0 + b}")
 
 
 # ---------------------------------------------------------------- varlen prefill
@@ -809,3 +810,31 @@ def test_fixed_length_many_units(fa, mode):
             out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, cl, 1024, 64)
             ref = A.decode_sliding_window(q, k, v, cl, 1024, 64)
     assert_close(out, ref, what=f"{mode} many units")
+
+
+@pytest.mark.parametrize("mode", ["decode", "window", "int8"])
+@pytest.mark.parametrize("d,n", [(64, 2049), (256, 2049), (64, 3329), (256, 3329), (128, 3329)])
+def test_fixed_length_lds_k_head_dims(fa, mode, d, n):
+    """B=16, 32:8 heads: 128 units in 4 (n=2049) or 5 (n=3329, an odd split
+    count) splits, i.e. 512-640 workgroups, the launches that stage K in LDS by
+    row-coalesced copies; D=64 (two rows per swizzle) and D=256 (two copies per
+    row) take other copy shapes than D=128.  Every output row against the oracle."""
+    b, hq, hkv = 16, 32, 8
+    cl = n - 1
+    g = gen(7000 + d + n + len(mode))
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, n, d), randn(g, b, hkv, n, d)
+    if mode == "decode":
+        out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, cl)
+        assert_close(out, A.decode(q, k, v, True, cl), what=f"decode d={d} n={n}")
+    elif mode == "window":
+        out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, cl, n - 100, 64)
+        assert_close(out, A.decode_sliding_window(q, k, v, cl, n - 100, 64), what=f"window d={d} n={n}")
+    else:
+        qs = (q.float().abs().amax(-1).squeeze(-1) / 127).contiguous()
+        ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(b, hkv, n).contiguous()
+        out = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), cl)
+        ref = A.decode_int8(q, k, v, qs, ks, cl)
+        assert rel_l2(out, ref) <= INT8_REL_L2
+        # per row as well: a wrong row cannot hide in the global norm
+        for bb in range(b):
+            assert rel_l2(out[bb:bb + 1], ref[bb:bb + 1]) <= INT8_REL_L2, f"int8 d={d} n={n} row {bb}"
