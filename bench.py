@@ -51,7 +51,54 @@ def parse():
     ap.add_argument("--configs", default="1,2,3,4,5a,5b,6a,6b,7,7b,8,9")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
+    ap.add_argument("--ceilings", action="store_true",
+                    help="also measure the streaming-read and MFMA-chain ceilings (libfa_ceilings.so)")
+    ap.add_argument("--record-traffic", nargs=2, type=float, metavar=("FETCH_KIB", "WRITE_KIB"),
+                    help="write profiles/traffic.json for the headline kernel from the FETCH_SIZE and "
+                         "WRITE_SIZE per-dispatch means (KiB) of two rocprofv3 --pmc passes, stamped "
+                         "with the hash of the sources that build it, and exit")
     return ap.parse_args()
+
+
+# Sources the headline kernel is built from: roofline.traffic is reported only
+# while profiles/traffic.json carries the hash of these files as they are now.
+TRAFFIC_SOURCES = ("flash_attn_v100_amd/csrc/decode.hip", "flash_attn_v100_amd/csrc/common.h",
+                   "flash_attn_v100_amd/csrc/capi_internal.h")
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0  # counter calibration against a 1 GiB copy
+
+
+def traffic_source_hash():
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(REPO, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def record_traffic(fetch_kib, write_kib):
+    entry = {"workload": "config 2", "fetch_kib_per_dispatch": fetch_kib, "write_kib_per_dispatch": write_kib,
+             "fetch_scale": FETCH_SCALE, "write_scale": WRITE_SCALE,
+             "hbm_bytes_per_launch": round((fetch_kib * FETCH_SCALE + write_kib * WRITE_SCALE) * 1024),
+             "source_sha256": traffic_source_hash(), "sources": list(TRAFFIC_SOURCES)}
+    with open(os.path.join(REPO, "profiles", "traffic.json"), "w") as f:
+        json.dump({HEADLINE_KERNEL: entry}, f, indent=2)
+        f.write("\n")
+    print(json.dumps(entry))
+
+
+def load_traffic():
+    """(bytes per launch, stale flag) for the headline kernel; bytes is None when
+    the file is missing or was measured on other sources than the ones built now."""
+    tpath = os.path.join(REPO, "profiles", "traffic.json")
+    if not os.path.exists(tpath):
+        return None, True
+    with open(tpath) as f:
+        entry = json.load(f).get(HEADLINE_KERNEL, {})
+    if entry.get("source_sha256") != traffic_source_hash():
+        return None, True
+    return entry.get("hbm_bytes_per_launch"), False
 
 
 def time_gpu(fn, steps, warmup):
@@ -352,6 +399,55 @@ def cfg9_speculative_verify(fa, torch, steps, warmup):
                 bound="serial fp32 running sums (latency)"), (tp[:2].cpu(), dp[:2].cpu(), tok[:2].cpu(), rv[:2].cpu(), K)
 
 
+# ----------------------------------------------------------------------------- ceilings
+
+def measure_ceilings(torch):
+    """Streaming-read and MFMA-chain ceilings from libfa_ceilings.so (csrc/ceilings.hip):
+    the rates the part sustains for the two rooflines, next to the published peaks."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(REPO, "flash_attn_v100_amd", "libfa_ceilings.so"))
+    st = torch.cuda.current_stream()
+    out = {}
+
+    def timed(fn, calls):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(calls):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / calls
+
+    nbytes = 4 << 30  # 16x the 256 MB MALL
+    src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda")
+    for blocks in (2048, 8192):
+        sink = torch.empty(blocks * 256 * 16, dtype=torch.uint8, device="cuda")
+        sec = timed(lambda: lib.fa_ceiling_stream_read(ctypes.c_void_p(src.data_ptr()), ctypes.c_size_t(nbytes),
+                                                       ctypes.c_void_p(sink.data_ptr()), blocks,
+                                                       ctypes.c_void_p(st.cuda_stream)), 20)
+        out[f"stream_read_{blocks}wg"] = dict(gbs=nbytes / sec / 1e9, frac_of_peak=nbytes / sec / 1e9 / HBM_PEAK_GBS,
+                                              bytes=nbytes, us=sec * 1e6)
+    del src
+    iters = 4000
+    g = torch.Generator(device="cuda").manual_seed(11)
+    for blocks in (256 * 2, 256 * 3):  # 2 or 3 waves per SIMD, each with 4 independent accumulators
+        n = blocks * 4 * 16 * 64 * 8
+        flops = blocks * 4 * iters * 8 * 32768.0
+        for name, ops in (("random_normal", torch.randn(n, generator=g, device="cuda").half()),
+                          ("constant", torch.full((n,), 0.5, device="cuda").half())):
+            sink = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+            sec = timed(lambda: lib.fa_ceiling_mfma_chain(ctypes.c_void_p(ops.data_ptr()), iters,
+                                                          ctypes.c_void_p(sink.data_ptr()), blocks,
+                                                          ctypes.c_void_p(st.cuda_stream)), 10)
+            out[f"mfma_f16_{name}_{blocks // 256}wps"] = dict(
+                tflops=flops / sec / 1e12, frac_of_peak=flops / sec / 1e12 / MFMA_FP16_PEAK_TFS, us=sec * 1e6)
+    return out
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 def cpu_baseline_cfg2(torch, sample, budget_s=12.0):
@@ -457,6 +553,9 @@ def cpu_baseline_sampled(torch, results, samples, budget_s=6.0):
 
 def main():
     args = parse()
+    if args.record_traffic:
+        record_traffic(*args.record_traffic)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build runs on one GPU only; sharding over several GPUs is a "
                                    "design, not a measured path", "n_gpus": args.gpus}))
@@ -468,7 +567,7 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.backends.cuda.matmul.allow_tf32 = False
-    want = [c.strip() for c in args.configs.split(",") if c.strip()]
+    want = [c.strip() for c in args.configs.split(",") if c.strip() and c.strip() != "none"]
     if args.only_headline:
         want = ["2"]
     results, samples = {}, {}
@@ -479,10 +578,12 @@ def main():
             "6a": (100, 10), "6b": (100, 10), "7": (20, 3), "7b": (5, 1), "8": (100, 10), "9": (50, 5)}
 
     def counts(c):
+        # config 2 (the headline step) times exactly --steps calls; every other
+        # config times at least 20 calls, whatever --steps asks for
         st, wu = base[c]
         if c == "2":
             return args.steps, args.warmup
-        return max(1, round(st * args.steps / 200)), max(1, round(wu * args.warmup / 20))
+        return max(20, round(st * args.steps / 200)), max(1, round(wu * args.warmup / 20))
 
     runners = {
         "1": lambda st, wu: cfg1_prefill(fa, torch, st, wu),
@@ -522,15 +623,16 @@ def main():
         for c, r in cpu_other.items():
             results[c]["cpu"] = r
 
+    ceilings = None
+    if args.ceilings:
+        log("ceilings ...")
+        ceilings = measure_ceilings(torch)
+        log("ceilings: " + json.dumps(ceilings))
     if "2" not in results:  # partial run (e.g. under a profiler): per-config figures only
-        print(json.dumps({"configs": results}), flush=True)
+        print(json.dumps({"configs": results, "ceilings": ceilings}), flush=True)
         return
     head = results["2"]
-    traffic = None
-    tpath = os.path.join(REPO, "profiles", "traffic.json")
-    if os.path.exists(tpath):  # measured by the rocprofv3 --pmc passes summarised beside it
-        with open(tpath) as f:
-            traffic = json.load(f).get(HEADLINE_KERNEL, {}).get("hbm_bytes_per_launch")
+    traffic, traffic_stale = load_traffic()  # measured by the rocprofv3 --pmc passes summarised beside it
     line = {
         "metric": "decode GQA attn HBM GB/s (% of peak); prefill fp16 TFLOP/s (% MFMA peak)",
         "value": round(head["gbs"], 2),
@@ -548,9 +650,11 @@ def main():
                    "seq_len": 4097, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_stale": traffic_stale,
                      "kernel": HEADLINE_KERNEL, "avg_launch_us": round(head["ms"] * 1e3, 3),
                      "timing": "HIP events on the launch stream around %d back-to-back calls" % args.steps},
         "cpu_baseline": cpu,
+        "ceilings": ceilings,
         "configs": {c: {k: (round(v, 6) if isinstance(v, float) else v) for k, v in r.items()}
                     for c, r in results.items()},
     }

@@ -3,6 +3,7 @@
 Produces, next to this file:
   libflash_attn_mi355x.so   HIP kernels + C ABI (include/flash_attn_mi355x.h), gfx950
   _flash_attn_v100*.so      PyTorch-ROCm extension exposing the reference API
+  libfa_ceilings.so         roofline probes used by bench.py --ceilings (not the library)
 
 Run ``python flash_attn_v100_amd/build.py`` (or ``__graft_entry__.build()``); it is a
 standalone script so it works before the package is importable.
@@ -22,6 +23,7 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libflash_attn_mi355x.so"
+CEILINGS_LIB = "libfa_ceilings.so"
 EXT_NAME = "_flash_attn_v100"
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
@@ -93,6 +95,16 @@ def build_library(verbose: bool = True) -> str:
     return out
 
 
+def build_ceilings(verbose: bool = True) -> str:
+    """Compile the roofline probes (csrc/ceilings.hip) into libfa_ceilings.so,
+    a separate library that only bench.py --ceilings loads."""
+    out = os.path.join(PKG_DIR, CEILINGS_LIB)
+    _run([HIPCC, *HIP_FLAGS, "-shared", os.path.join(CSRC, "ceilings.hip"), "-o", out])
+    if verbose:
+        print(f"[build] {out}")
+    return out
+
+
 def build_extension(verbose: bool = True) -> str:
     """Compile the pybind11/ATen binding against torch and link the C-ABI library."""
     import torch
@@ -126,6 +138,7 @@ def build_extension(verbose: bool = True) -> str:
 def build_all(verbose: bool = True) -> None:
     build_library(verbose)
     build_extension(verbose)
+    build_ceilings(verbose)
 
 
 if __name__ == "__main__":
