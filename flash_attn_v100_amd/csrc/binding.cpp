@@ -49,74 +49,81 @@ int to_int(int64_t x, const char* what) {
   return static_cast<int>(x);
 }
 
+// Shape agreement between q, k and v, as rule tables: each rule names one
+// dimension (or the whole shape), the tensor pairs that must agree on it, and
+// the message the reference raises when they do not.  The conditions and
+// messages follow the reference's validators (flash_attn_kernel.cu:122-249);
+// the table form is this build's own.
+constexpr unsigned kQK = 1u, kQV = 2u, kKV = 4u;  // pairs: (q, k), (q, v), (k, v)
+constexpr int kWholeShape = -1;
+
+struct Agree {
+  int dim;         // dimension index, or kWholeShape
+  unsigned pairs;  // kQK | kQV | kKV
+  const char* msg;
+};
+
+// self-attention: q, k, v of one shape
+constexpr Agree kMhaRules[] = {{kWholeShape, kQK, "q and k must have the same shape"},
+                               {kWholeShape, kQV, "q and v must have the same shape"}};
+// MHA decode: q [B, H, 1, D] against k, v [B, H, N, D]
+constexpr Agree kDecodeMhaRules[] = {{0, kQK | kQV, "q, k, v batch size must match"},
+                                     {1, kQK | kQV, "q, k, v head count must match"},
+                                     {3, kQK | kQV, "q, k, v head dimension must match"},
+                                     {2, kKV, "k and v sequence length must match"}};
+// GQA prefill: k, v may have fewer heads than q
+constexpr Agree kPrefillGqaRules[] = {{0, kQK | kQV, "q, k, v batch size must match"},
+                                      {1, kKV, "k and v must have the same number of heads"},
+                                      {2, kQK | kQV, "q, k, v sequence length must match"},
+                                      {3, kQK | kQV, "q, k, v head dimension must match"}};
+// GQA decode
+constexpr Agree kDecodeGqaRules[] = {{0, kQK | kQV, "q, k, v batch size must match"},
+                                     {1, kKV, "k and v must have the same number of heads"},
+                                     {2, kKV, "k and v sequence length must match"},
+                                     {3, kQK | kQV, "q, k, v head dimension must match"}};
+// packed varlen: [total, H, D] each
+constexpr Agree kVarlenRules[] = {{0, kQK | kQV, "k and v total length must match q"},
+                                  {1, kQK | kQV, "k and v head count must match q"},
+                                  {2, kQK | kQV, "k and v head dimension must match q"}};
+
+template <size_t N>
+void check_qkv(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, int64_t ndim,
+               const Agree (&rules)[N]) {
+  const at::Tensor* t[3] = {&q, &k, &v};
+  const char* name[3] = {"q", "k", "v"};
+  for (int i = 0; i < 3; ++i) TORCH_CHECK(t[i]->dim() == ndim, name[i], " must be a ", ndim, "D tensor");
+  for (int i = 1; i < 3; ++i) TORCH_CHECK(t[i]->device() == q.device(), "q and ", name[i], " must be on the same device");
+  for (int i = 1; i < 3; ++i) TORCH_CHECK(t[i]->dtype() == q.dtype(), "q and ", name[i], " must have the same dtype");
+  static constexpr int kPair[3][2] = {{0, 1}, {0, 2}, {1, 2}};
+  for (const Agree& r : rules) {
+    bool ok = true;
+    for (int pi = 0; pi < 3; ++pi) {
+      if (!(r.pairs & (1u << pi))) continue;
+      const at::Tensor& a = *t[kPair[pi][0]];
+      const at::Tensor& b = *t[kPair[pi][1]];
+      ok = ok && (r.dim == kWholeShape ? a.sizes() == b.sizes() : a.size(r.dim) == b.size(r.dim));
+    }
+    TORCH_CHECK(ok, r.msg);
+  }
+}
+
 void check_mha_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-  CHECK_DIM(q, 4);
-  CHECK_DIM(k, 4);
-  CHECK_DIM(v, 4);
-  CHECK_SAME_DEVICE(q, k);
-  CHECK_SAME_DEVICE(q, v);
-  CHECK_SAME_DTYPE(q, k);
-  CHECK_SAME_DTYPE(q, v);
-  TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape");
-  TORCH_CHECK(q.sizes() == v.sizes(), "q and v must have the same shape");
+  check_qkv(q, k, v, 4, kMhaRules);
 }
-
 void check_decode_mha_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-  CHECK_DIM(q, 4);
-  CHECK_DIM(k, 4);
-  CHECK_DIM(v, 4);
-  CHECK_SAME_DEVICE(q, k);
-  CHECK_SAME_DEVICE(q, v);
-  CHECK_SAME_DTYPE(q, k);
-  CHECK_SAME_DTYPE(q, v);
-  TORCH_CHECK(q.size(0) == k.size(0) && q.size(0) == v.size(0), "q, k, v batch size must match");
-  TORCH_CHECK(q.size(1) == k.size(1) && q.size(1) == v.size(1), "q, k, v head count must match");
-  TORCH_CHECK(q.size(3) == k.size(3) && q.size(3) == v.size(3), "q, k, v head dimension must match");
-  TORCH_CHECK(k.size(2) == v.size(2), "k and v sequence length must match");
+  check_qkv(q, k, v, 4, kDecodeMhaRules);
 }
-
 void check_prefill_gqa_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-  CHECK_DIM(q, 4);
-  CHECK_DIM(k, 4);
-  CHECK_DIM(v, 4);
-  CHECK_SAME_DEVICE(q, k);
-  CHECK_SAME_DEVICE(q, v);
-  CHECK_SAME_DTYPE(q, k);
-  CHECK_SAME_DTYPE(q, v);
-  TORCH_CHECK(q.size(0) == k.size(0) && q.size(0) == v.size(0), "q, k, v batch size must match");
-  TORCH_CHECK(k.size(1) == v.size(1), "k and v must have the same number of heads");
-  TORCH_CHECK(q.size(2) == k.size(2) && q.size(2) == v.size(2), "q, k, v sequence length must match");
-  TORCH_CHECK(q.size(3) == k.size(3) && q.size(3) == v.size(3), "q, k, v head dimension must match");
+  check_qkv(q, k, v, 4, kPrefillGqaRules);
 }
-
 void check_decode_gqa_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v) {
-  CHECK_DIM(q, 4);
-  CHECK_DIM(k, 4);
-  CHECK_DIM(v, 4);
-  CHECK_SAME_DEVICE(q, k);
-  CHECK_SAME_DEVICE(q, v);
-  CHECK_SAME_DTYPE(q, k);
-  CHECK_SAME_DTYPE(q, v);
-  TORCH_CHECK(q.size(0) == k.size(0) && q.size(0) == v.size(0), "q, k, v batch size must match");
-  TORCH_CHECK(k.size(1) == v.size(1), "k and v must have the same number of heads");
-  TORCH_CHECK(k.size(2) == v.size(2), "k and v sequence length must match");
-  TORCH_CHECK(q.size(3) == k.size(3) && q.size(3) == v.size(3), "q, k, v head dimension must match");
+  check_qkv(q, k, v, 4, kDecodeGqaRules);
 }
-
 void check_varlen_prefill_input_shapes(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                        const at::Tensor& cu_seqlens) {
-  CHECK_DIM(q, 3);
-  CHECK_DIM(k, 3);
-  CHECK_DIM(v, 3);
   CHECK_DIM(cu_seqlens, 1);
-  CHECK_SAME_DEVICE(q, k);
-  CHECK_SAME_DEVICE(q, v);
   CHECK_SAME_DEVICE(q, cu_seqlens);
-  CHECK_SAME_DTYPE(q, k);
-  CHECK_SAME_DTYPE(q, v);
-  TORCH_CHECK(k.size(0) == q.size(0) && v.size(0) == q.size(0), "k and v total length must match q");
-  TORCH_CHECK(k.size(1) == q.size(1) && v.size(1) == q.size(1), "k and v head count must match q");
-  TORCH_CHECK(k.size(2) == q.size(2) && v.size(2) == q.size(2), "k and v head dimension must match q");
+  check_qkv(q, k, v, 3, kVarlenRules);
 }
 
 void check_cache_len(int cache_len, int64_t seq_len) {

@@ -68,6 +68,9 @@ constexpr int kTargetBlocksFixed = FA_DEC_TARGET_BLOCKS_FIXED;
 constexpr int kFixedQuantum = 256;  // fixed-length split boundaries (kSmallGridQuantum below)
 constexpr int kMaxSplits = 128;
 constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this many units run split-major
+#ifndef FA_DEC_PEEK
+#define FA_DEC_PEEK 1
+#endif
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
 struct DecodeParams {
@@ -792,6 +795,26 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
 
   bool bad = false;
   if constexpr (MODE == kModePaged) bad = s_bad != 0;
+  // Peek (fixed-length launches that stage K in LDS, split-major): a split
+  // that finds every other split of its unit already arrived is the merger;
+  // it keeps its own partial in LDS (the K staging buffer, free after the
+  // walk) instead of writing it out, waiting for the writes and taking an
+  // arrival rank, i.e. one device round trip less on the path of the split
+  // that finishes last.  Others publish as usual after the peek.
+  constexpr bool kPeek = FA_DEC_PEEK && kLdsK && kFixedLen;
+  __shared__ int s_peek;
+  bool merger_now = false;
+  float* own = reinterpret_cast<float*>(s_k);  // [GB][DP] partial, then [GB] log2-sum-exp
+  static_assert(!kPeek || sizeof(s_k) >= (GB * DP + GB) * sizeof(float), "own partial fits the K buffer");
+  if constexpr (kPeek) {
+    if (split_major && sb > 1) {
+      if (tid == 0)
+        s_peek = __hip_atomic_load(&p.counters[counter_index(slot)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 static_cast<unsigned>(sb - 1);
+      __syncthreads();
+      merger_now = s_peek != 0;
+    }
+  }
   // One thread per (head, 4 columns): every LDS read of the wave merge is
   // issued at once, then one 16-byte store of the split's partial.
   constexpr int NC4 = DP / 4;
@@ -830,6 +853,9 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         if (d4 + j < D) op[j] = static_cast<half_t>(outv[j]);
+    } else if (kPeek && merger_now) {
+      *reinterpret_cast<float4_t*>(&own[g * DP + d4]) = outv;
+      if (d4 == 0) own[GB * DP + g] = lse;
     } else {
       const size_t e = bh * S + split;
       store_coherent4(&p.ws_o[e * DP + d4], outv);
@@ -845,14 +871,18 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // unit's counter; the split with the last rank finds every other partial
   // complete and merges at once.
   __shared__ int s_last;
-  wait_vmem_stores();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
-    s_last = (arrival == static_cast<unsigned>(sb - 1));
+  if (kPeek && merger_now) {
+    __syncthreads();  // the own partial is in LDS
+  } else {
+    wait_vmem_stores();
+    __syncthreads();
+    if (tid == 0) {
+      const unsigned arrival = atomicAdd(&p.counters[counter_index(slot)], 1u);
+      s_last = (arrival == static_cast<unsigned>(sb - 1));
+    }
+    __syncthreads();
+    if (!s_last) return;
   }
-  __syncthreads();
-  if (!s_last) return;
   // Every split of the unit has taken its arrival rank: the counter can go
   // back to zero for the next call on this workspace.
   if (tid == 0) __hip_atomic_store(&p.counters[counter_index(slot)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -882,6 +912,11 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // loads split sp of column c into (v, l)
   auto load_split = [&](int c, int sp, float4_t& v, float& l) {
     const int g = c / (DP / 4), d4 = (c % (DP / 4)) * 4;
+    if (kPeek && merger_now && sp == split) {
+      v = *reinterpret_cast<const float4_t*>(&own[g * DP + d4]);
+      l = own[GB * DP + g];
+      return;
+    }
     v = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(
                                          ws_rsrc, ((g * S + sp) * DP + d4) * static_cast<int>(sizeof(float)), 0, 16));
     l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
@@ -1161,12 +1196,22 @@ using namespace fa;
 
 extern "C" size_t fa_decode_workspace_size(int B, int H_Q, int H_KV, int max_len, int D) {
   if (B <= 0 || H_Q <= 0 || H_KV <= 0 || D <= 0 || D > 256 || H_Q % H_KV != 0) return 0;
-  // Large enough for the plan of every mode: the per-sequence plan (most
-  // workgroups) and the fixed-length plan (finest split quantum).
-  const size_t a = plan_layout(make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocks), B, H_Q, H_KV).total;
-  const size_t b = plan_layout(make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocksFixed, true, kSmallGridQuantum), B,
-                               H_Q, H_KV).total;
-  return a > b ? a : b;
+  // Large enough for the plan of every mode at every key count up to max_len.
+  // The split count is not monotonic in the key count (the chunk rounds up to
+  // a quantum: 128 units of 1280 keys split 5 ways, of 1281 keys 3 ways), so
+  // this bounds it instead of planning max_len: a plan with target T over u
+  // units has chunk >= L u / T, hence at most ceil(T / u) splits (or
+  // ceil(L / kMaxChunk) once the chunk is capped), and never more than
+  // ceil(L / quantum) with the smallest quantum, nor more than kMaxSplits.
+  DecodePlan pl = make_plan(B, H_Q, H_KV, max_len, D, kTargetBlocks);
+  const long long units = static_cast<long long>(B) * H_KV * pl.num_hg;
+  const long long tmax = std::max(kTargetBlocks, kTargetBlocksFixed);
+  const long long L = std::max(max_len, 1);
+  long long s = std::max((tmax + units - 1) / units, (L + kMaxChunk - 1) / kMaxChunk);
+  s = std::min(s, (L + kSmallGridQuantum - 1) / kSmallGridQuantum);
+  s = std::min(s, static_cast<long long>(kMaxSplits));
+  pl.splits = static_cast<int>(s);
+  return plan_layout(pl, B, H_Q, H_KV).total;
 }
 
 extern "C" int fa_decode_fp16(const void* q, const void* k, const void* v, void* o, int B, int H_Q,

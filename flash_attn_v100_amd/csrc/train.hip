@@ -3,6 +3,7 @@
 // forward kernels (built with MFMA accumulators in VGPRs; the fp32 backward
 // lives in train_fp32.hip).
 #include <mutex>
+#include <vector>
 
 #include "capi_internal.h"
 #include "train_kernels.h"
@@ -10,22 +11,43 @@
 namespace fa {
 namespace train {
 
-hipStream_t backward_side_stream(int which) {
+hipStream_t backward_side_stream(hipStream_t caller, int which) {
+  // Side streams per (device, caller stream): backward calls issued on
+  // different caller streams (threads, serving loops) keep their concurrency
+  // instead of queueing on one shared pair.  At most kMaxCallers pairs per
+  // device are made; past that the oldest pair is handed to the new caller
+  // (its work then queues behind the other caller's, which is still correct).
+  // Streams are never destroyed, so a pair handed over can have work pending.
   constexpr int kMaxDevices = 64;
+  constexpr size_t kMaxCallers = 16;
+  struct Entry {
+    hipStream_t caller;
+    hipStream_t side[2];
+  };
   static std::mutex mu;
-  static hipStream_t streams[kMaxDevices][2] = {};
+  static std::vector<Entry> pairs[kMaxDevices];
+  static size_t next_reuse[kMaxDevices] = {};
   int dev = 0;
   if (which < 0 || which > 1 || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(mu);
-  if (streams[dev][which] == nullptr) {
-    hipStream_t s = nullptr;
-    if (hipStreamCreateWithFlags(&s, hipStreamNonBlocking) != hipSuccess) {
+  std::vector<Entry>& list = pairs[dev];
+  for (Entry& e : list)
+    if (e.caller == caller) return e.side[which];
+  if (list.size() >= kMaxCallers) {
+    Entry& e = list[next_reuse[dev]++ % list.size()];
+    e.caller = caller;
+    return e.side[which];
+  }
+  Entry e = {caller, {nullptr, nullptr}};
+  for (int i = 0; i < 2; ++i) {
+    if (hipStreamCreateWithFlags(&e.side[i], hipStreamNonBlocking) != hipSuccess) {
       (void)hipGetLastError();  // leave no sticky error for check_launch
+      if (i == 1) (void)hipStreamDestroy(e.side[0]);
       return nullptr;
     }
-    streams[dev][which] = s;
   }
-  return streams[dev][which];
+  list.push_back(e);
+  return e.side[which];
 }
 
 bool backward_events(hipEvent_t (&ev)[4]) {

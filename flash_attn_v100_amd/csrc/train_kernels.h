@@ -797,9 +797,10 @@ __global__ __launch_bounds__(256) void delta_kernel(TrainParams p) {
 // and train_fp32.hip; the fp32 forward, which fits 256 VGPRs, by train.hip).
 
 // Non-blocking, default-priority streams (which = 0, 1) of the current
-// device for the backward's concurrent passes (created on first use, kept for
-// the process; nullptr if one cannot be created).  Defined in train.hip.
-hipStream_t backward_side_stream(int which);
+// device for the concurrent passes of a backward issued on `caller`: one pair
+// per caller stream (created on first use, kept for the process; nullptr if
+// one cannot be created).  Defined in train.hip.
+hipStream_t backward_side_stream(hipStream_t caller, int which);
 // The calling thread's four fork/join events for the current device (created
 // once, reused by every later backward call of that thread); false if they
 // cannot be made.
@@ -822,8 +823,8 @@ void launch_backward_dp(const TrainParams& p, hipStream_t st) {
     // into a graph: the capture then keeps the launches in order on `st`.)
     hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(st, &capture) != hipSuccess || capture != hipStreamCaptureStatusNone;
-    hipStream_t side_v = capturing || !kSplit ? nullptr : backward_side_stream(0);
-    hipStream_t side_k = capturing ? nullptr : backward_side_stream(1);
+    hipStream_t side_v = capturing || !kSplit ? nullptr : backward_side_stream(st, 0);
+    hipStream_t side_k = capturing ? nullptr : backward_side_stream(st, 1);
     hipEvent_t ev[4] = {};  // fork, delta ready, dV done, dK(/dV) done
     bool ok = side_k != nullptr && (!kSplit || side_v != nullptr) && backward_events(ev);
     if (kSplit)

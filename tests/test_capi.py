@@ -62,6 +62,18 @@ def test_workspace_size_plan(lib):
     assert lib.fa_decode_workspace_size(1, 6, 4, 65, 64) == 0              # invalid group -> 0
 
 
+def test_workspace_size_bounds_every_shorter_key_count(lib):
+    """The split count is not monotonic in the key count (the split length rounds
+    up to a quantum), while the bindings size the workspace by N and a call may
+    attend fewer keys (sliding window, cache_len < N - 1).  The size for N must
+    cover every key count up to N."""
+    for b, hq, hkv, d in ((16, 32, 8, 128), (16, 32, 8, 64), (16, 32, 8, 256), (1, 32, 8, 128), (64, 32, 8, 128),
+                          (128, 32, 8, 128), (4, 64, 2, 128)):
+        sizes = [lib.fa_decode_workspace_size(b, hq, hkv, n, d) for n in range(1, 4200, 7)]
+        for i in range(1, len(sizes)):
+            assert sizes[i] >= max(sizes[:i]), (b, hq, hkv, d, 1 + 7 * i)
+
+
 def _vp(x=0):
     return ctypes.c_void_p(x)
 

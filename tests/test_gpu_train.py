@@ -204,3 +204,32 @@ def test_backward_concurrent_streams_and_graph_capture(fa, dtype, d):
         torch.cuda.synchronize()
         for x, y in zip(captured, eager):
             assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_backward_on_several_caller_streams(fa, dtype):
+    """Backward calls issued on different caller streams at once (each with its
+    own pair of side streams for the concurrent passes) give exactly the
+    results of the same calls run one after another on the default stream."""
+    b, h, n, d = 1, 4, 384, 128
+    g = gen(4040)
+    cases = []
+    for i in range(4):
+        q, k, v, do = (randn(g, b, h, n, d, dtype=dtype).cuda() for _ in range(4))
+        fwd = fa.forward_fp16_with_lse if dtype == torch.float16 else fa.forward_with_lse
+        out, lse = fwd(q, k, v, True)
+        cases.append((do, q, k, v, out, lse))
+    torch.cuda.synchronize()
+    ref = [fa.backward(*c, True) for c in cases]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in cases]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    got = []
+    for s, c in zip(streams, cases):
+        with torch.cuda.stream(s):
+            got.append(fa.backward(*c, True))
+    torch.cuda.synchronize()
+    for r, x in zip(ref, got):
+        for a, e in zip(x, r):
+            assert torch.equal(a, e)
