@@ -65,7 +65,17 @@ constexpr int kTargetBlocksPaged = FA_DEC_TARGET_BLOCKS / FA_DEC_PAGED_DIV;
 #define FA_DEC_TARGET_BLOCKS_FIXED 640
 #endif
 constexpr int kTargetBlocksFixed = FA_DEC_TARGET_BLOCKS_FIXED;
-constexpr int kFixedQuantum = 256;  // fixed-length split boundaries (kSmallGridQuantum below)
+#ifndef FA_DEC_FIXED_QUANTUM
+#define FA_DEC_FIXED_QUANTUM 256
+#endif
+constexpr int kFixedQuantum = FA_DEC_FIXED_QUANTUM;  // fixed-length split boundaries (kSmallGridQuantum below)
+// The INT8 KV cache reads half the bytes per key and dequantizes them with a
+// few packed fp16 ops, so its splits are cheaper than the fp16 modes': finer
+// ones (128-key quantum, about three workgroups per CU) balance better there
+// (6a 18.8 -> 18.2 us; the same plan made 5b and 6b slower, 29.0 -> 29.6-30.1
+// and 26.5 -> 27.1 us).
+constexpr int kTargetBlocksInt8KV = 768;
+constexpr int kInt8KVQuantum = 128;
 constexpr int kMaxSplits = 128;
 constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this many units run split-major
 #ifndef FA_DEC_PEEK
@@ -1121,7 +1131,13 @@ static int check_common(const char* fn, int B, int H_Q, int H_KV, int D) {
 
 template <int MODE>
 static int target_blocks() {
+  if constexpr (MODE == kModeInt8KV) return kTargetBlocksInt8KV;
   return MODE == kModePaged ? kTargetBlocksPaged : (MODE == kModeCB ? kTargetBlocks : kTargetBlocksFixed);
+}
+// Split quantum of a fixed-length mode.
+template <int MODE>
+static int fixed_quantum() {
+  return MODE == kModeInt8KV ? kInt8KVQuantum : kFixedQuantum;
 }
 
 // The split plan of a call.  Fixed-length calls split at multiples of
@@ -1136,7 +1152,7 @@ template <int MODE>
 static DecodePlan plan_for(int B, int H_Q, int H_KV, int max_len, int D) {
   constexpr bool kFixed = MODE == kModeDecode || MODE == kModeInt8 || MODE == kModeInt8KV;
   if (!kFixed) return make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), false, kChunkQuantum);
-  DecodePlan pl = make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), true, kFixedQuantum);
+  DecodePlan pl = make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), true, fixed_quantum<MODE>());
   const long long blocks = static_cast<long long>(B) * H_KV * pl.num_hg * pl.splits;
   if (blocks < kSmallGridBlocks) pl = make_plan(B, H_Q, H_KV, max_len, D, target_blocks<MODE>(), true, kSmallGridQuantum);
   return pl;
