@@ -118,7 +118,9 @@ struct DecodeParams {
 // each before the first key load can issue.
 template <int MODE>
 __device__ __forceinline__ void preload_args(const DecodeParams& p) {
-  asm volatile("" ::"s"(p.q), "s"(p.o), "s"(p.ws_o), "s"(p.ws_lse), "s"(p.counters));
+  // gridDim.x (a hidden kernel argument) too: the split-major test needs it,
+  // and fetched on its own it was a second dependent round trip
+  asm volatile("" ::"s"(p.q), "s"(p.o), "s"(p.ws_o), "s"(p.ws_lse), "s"(p.counters), "s"(gridDim.x));
   asm volatile("" ::"s"(p.unit_base), "s"(p.B), "s"(p.H_Q), "s"(p.H_KV),
                "s"(p.N), "s"(p.D), "s"(p.G));
   asm volatile("" ::"s"(p.chunk), "s"(p.num_splits), "s"(p.num_hg), "s"(p.absorb_tail), "s"(p.scale_log2));

@@ -838,3 +838,30 @@ def test_fixed_length_lds_k_head_dims(fa, mode, d, n):
         # per row as well: a wrong row cannot hide in the global norm
         for bb in range(b):
             assert rel_l2(out[bb:bb + 1], ref[bb:bb + 1]) <= INT8_REL_L2, f"int8 d={d} n={n} row {bb}"
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_continuous_batching_many_splits_head_dims(fa, d):
+    """Continuous batching (K staged in LDS) at D=64 and D=256 with sequences long
+    enough for several splits each, plus an empty and a one-key sequence;
+    every output row against the oracle."""
+    g = gen(900 + d)
+    b, hq, hkv, max_n = 6, 16, 4, 3001
+    cls = torch.tensor([3000, 1, 2047, -1, 1500, 2999], dtype=torch.int32)
+    q, k, v = randn(g, b, hq, 1, d), randn(g, b, hkv, max_n, d), randn(g, b, hkv, max_n, d)
+    out = fa.forward_continuous_batching_fp16(*cuda(q, k, v, cls), True)
+    assert_close(out, A.continuous_batching(q, k, v, cls, True), what=f"cb d={d}")
+
+
+@pytest.mark.parametrize("d", [64, 256])
+def test_paged_decode_many_splits_head_dims(fa, d):
+    """Paged decode at D=64 and D=256 over a random page permutation with
+    sequences of several splits (up to 3000 tokens)."""
+    g = gen(950 + d)
+    b, hq, hkv, mnb, npages = 5, 16, 4, 200, 1000
+    sl = torch.tensor([3000, 17, 1999, 16, 2500], dtype=torch.int32)
+    bt = torch.randperm(npages, generator=g)[: b * mnb].view(b, mnb).int()
+    kc, vc = randn(g, npages, hkv, 16, d), randn(g, npages, hkv, 16, d)
+    q = randn(g, b, hq, 1, d)
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, sl), mnb)
+    assert_close(out, A.paged_decode(q, kc, vc, bt, sl, mnb), what=f"paged d={d}")
