@@ -81,6 +81,9 @@ constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this 
 #ifndef FA_DEC_PEEK
 #define FA_DEC_PEEK 1
 #endif
+#ifndef FA_DEC_PIPE
+#define FA_DEC_PIPE 1
+#endif
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
 struct DecodeParams {
@@ -474,6 +477,34 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
       }
     }
   };
+  // Pipelined walk (continuous batching, and contiguous fp16 decode launches
+  // that stage K in LDS): V is staged in a second per-wave LDS buffer by the
+  // same kind of copies, lane i of copy u landing its 16 bytes (its own
+  // row-layout chunk) at u * 1024 + 16 i.  A tile's K fragments and V chunks
+  // are read into registers as soon as its copies have landed, and the next
+  // tile's copies are issued at once, so they travel while this tile's
+  // scores, softmax and P V are computed.
+  // (Config 3 186 -> 182 us, sliding-window B = 16 26.5 -> 26.1 us.  Paged
+  // decode measured slower with it, 179 -> 180.5 us: its 78 KB workgroups
+  // fit two per CU where three fit without; INT8 decode, 29.4 -> 30.6 us.)
+  constexpr bool kPipe = FA_DEC_PIPE && kLdsK && (MODE == kModeCB || MODE == kModeDecode);
+  __shared__ __attribute__((aligned(16))) half_t s_v[kPipe ? kDecWaves * TK * DP : 1];
+  const unsigned v_lds = static_cast<unsigned>(reinterpret_cast<uintptr_t>(
+                             (__attribute__((address_space(3))) half_t*)s_v)) + wave * (TK * DP * 2);
+  static_assert(!kPipe || UV * 1024 == TK * DP * 2, "V copy shape");
+  auto v_copy = [&](int t0) {
+    if constexpr (kPipe) {
+      const half_t* vh = p.v + kv_head_base;
+#pragma unroll
+      for (int u = 0; u < UV; ++u) {
+        const int t = min(t0 + u * RPW + rg, klast);
+        const int row = t < p.seg1 ? t : t + p.seg_shift;
+        const unsigned off = static_cast<unsigned>((row * D + col) * 2);
+        if constexpr (kStreamKV) copy16_to_lds_nt(vh, off, v_lds + u * 1024);
+        else copy16_to_lds(vh, off, v_lds + u * 1024);
+      }
+    }
+  };
   // K fragment (MFMA B operand) of 16-key tile tt, 32-column slice c
   auto k_frag = [&](int tt, int c) -> half8_t {
     const int r = 16 * tt + l16;
@@ -570,13 +601,13 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
       if constexpr (MODE == kModeInt8) {
         typedef int int4v __attribute__((ext_vector_type(4)));
         int4v ci = {0, 0, 0, 0};
-        if constexpr (kLdsK) {
+        if constexpr (kLdsK && !kPipe) {
           if (tt == 0) wait_vm<UV>();
         }
 #pragma unroll
         for (int c = 0; c < NC; c += 2) {
           int k0lo, k0hi, k1lo, k1hi;
-          if constexpr (kLdsK) {
+          if constexpr (kLdsK && !kPipe) {
             quant8(__builtin_bit_cast(u32x4, k_frag(tt, c)), inv_ks, k0lo, k0hi);
             quant8(__builtin_bit_cast(u32x4, k_frag(tt, c + 1)), inv_ks, k1lo, k1hi);
           } else {
@@ -592,7 +623,7 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
           sc[r] = static_cast<float>(ci[r]) * qsc[r] * ks * p.scale * kLog2e;
       } else {
         sc = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (kLdsK) {
+        if constexpr (kLdsK && !kPipe) {
           // this wave's K copies have landed once at most the UV later V loads are outstanding
           if (tt == 0) wait_vm<UV>();
 #pragma unroll
@@ -709,6 +740,38 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // tiles are locals of the loop body: kept in registers, not behind a
   // reference, or the compiler moves the INT8 scales to scratch memory.)
   auto walk = [&](int from, int to) {
+    if constexpr (kPipe) {
+      int t0 = from + wave * TK;
+      if (t0 >= to) return;
+      k_copy(t0);
+      v_copy(t0);
+      for (;;) {
+        // this wave's copies of tile t0 have landed (no other vector-memory
+        // operation is outstanding inside the walk)
+        wait_vm<0>();
+        Tile A;
+#pragma unroll
+        for (int tt = 0; tt < T16; ++tt)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) A.k[tt][c] = __builtin_bit_cast(u32x4, k_frag(tt, c));
+#pragma unroll
+        for (int u = 0; u < UV; ++u) A.v[u] = *lds_at<u32x4>(v_lds + u * 1024 + lane * 16);
+        const int tn = t0 + stride;
+        const bool more = tn < to;
+        if (more) {
+          // the reads above have returned before the buffers are overwritten
+          __builtin_amdgcn_sched_barrier(0);
+          wait_vm_lgkm0<63>();
+          k_copy(tn);
+          v_copy(tn);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        compute_tile(A, t0);
+        if (!more) break;
+        t0 = tn;
+      }
+      return;
+    }
     for (int t0 = from + wave * TK; t0 < to; t0 += stride) {
       Tile A;
       if constexpr (MODE == kModeInt8KV) {
@@ -754,7 +817,13 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   // ---- merge the waves through LDS ----
   __shared__ float s_m[kDecWaves][GP];
   __shared__ float s_l[kDecWaves][GP];
-  __shared__ __attribute__((aligned(16))) float s_acc[kDecWaves][GB][DP];
+  // The pipelined walk keeps its V buffers for the wave partials once every
+  // wave is done with them (two 80 KB workgroups per CU instead of one).
+  constexpr bool kAccInV = kPipe && GB * DP * 4 <= TK * DP * 2;
+  __shared__ __attribute__((aligned(16))) float s_acc_own[kAccInV ? 1 : kDecWaves * GB * DP];
+  typedef float AccBuf[kDecWaves][GB][DP];
+  AccBuf& s_acc = *reinterpret_cast<AccBuf*>(kAccInV ? reinterpret_cast<float*>(s_v) : s_acc_own);
+  if constexpr (kAccInV) __syncthreads();
   if (l16 == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
