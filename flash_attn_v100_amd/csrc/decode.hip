@@ -234,9 +234,9 @@ __device__ __forceinline__ int counter_index(int slot) {
 }
 
 template <int DP, int GB, int MODE, bool VEC, bool LDSK>
-// Three waves per SIMD (a 168-register budget): every mode's tile loop fits
-// it without spilling, and the compiler's own choice for the INT8 KV cache
-// (128 registers and a spill, for four waves) measured 14 % slower.
+// Registers are the compiler's choice under the 256-thread bound (94-256
+// VGPRs across the instantiations, none spilling); asking for four waves per
+// SIMD made the INT8 KV cache spill (128 registers) and run 14 % slower.
 __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
     DecodeParams p) {
   constexpr int NC = DP / 32;                 // 32-column slices of the QK^T product
