@@ -52,7 +52,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true", help="time config 2 only (for profilers)")
     ap.add_argument("--ceilings", action="store_true",
-                    help="also measure the streaming-read and MFMA-chain ceilings (libfa_ceilings.so)")
+                    help="measure the streaming-read and MFMA-chain ceilings (libfa_ceilings.so; the default)")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the ceilings (about a second of GPU time)")
     ap.add_argument("--record-traffic", nargs=2, type=float, metavar=("FETCH_KIB", "WRITE_KIB"),
                     help="write profiles/traffic.json for the headline kernel from the FETCH_SIZE and "
                          "WRITE_SIZE per-dispatch means (KiB) of two rocprofv3 --pmc passes, stamped "
@@ -624,7 +625,7 @@ def main():
             results[c]["cpu"] = r
 
     ceilings = None
-    if args.ceilings:
+    if not args.no_ceilings:
         log("ceilings ...")
         ceilings = measure_ceilings(torch)
         log("ceilings: " + json.dumps(ceilings))
@@ -652,6 +653,8 @@ def main():
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_stale": traffic_stale,
                      "kernel": HEADLINE_KERNEL, "avg_launch_us": round(head["ms"] * 1e3, 3),
+                     "frac_of_measured_stream_read": (round(head["gbs"] / ceilings["stream_read_2048wg"]["gbs"], 4)
+                                                      if ceilings else None),
                      "timing": "HIP events on the launch stream around %d back-to-back calls" % args.steps},
         "cpu_baseline": cpu,
         "ceilings": ceilings,
