@@ -812,6 +812,33 @@ def test_fixed_length_many_units(fa, mode):
     assert_close(out, ref, what=f"{mode} many units")
 
 
+def test_decode_more_units_than_counter_slots(fa):
+    """65537 (batch, head) units with two splits each: more units than the
+    workspace's 65536 arrival counters, so the call is issued as two launches
+    over unit ranges (the second reusing the counters the first left at zero).
+    Each half of the batch run as a call of its own (one launch, same split
+    plan) gives the same rows bit for bit; rows at the launch boundary and the
+    ends against the oracle.  D=8 keeps the 8256-key cache at 17 GB."""
+    b, n, d = 65537, 8256, 8
+    cl = n - 1
+    g = torch.Generator(device="cuda").manual_seed(65537)
+    q = torch.randn(b, 1, 1, d, generator=g, device="cuda", dtype=torch.float16)
+    k = torch.randn(b, 1, n, d, generator=g, device="cuda", dtype=torch.float16)
+    v = torch.randn(b, 1, n, d, generator=g, device="cuda", dtype=torch.float16)
+    out = fa.forward_decode_gqa_fp16(q, k, v, True, cl)
+    h = 32768
+    lo = fa.forward_decode_gqa_fp16(q[:h], k[:h], v[:h], True, cl)
+    hi = fa.forward_decode_gqa_fp16(q[h:], k[h:], v[h:], True, cl)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:h], lo)
+    assert torch.equal(out[h:], hi)
+    for row in (0, h - 1, h, 65535, 65536):
+        sl = slice(row, row + 1)
+        ref = A.decode(q[sl].cpu(), k[sl].cpu(), v[sl].cpu(), True, cl)
+        assert_close(out[sl], ref, what=f"decode row {row} of 65537 units")
+    del k, v
+
+
 @pytest.mark.parametrize("mode", ["decode", "window", "int8"])
 @pytest.mark.parametrize("d,n", [(64, 2049), (256, 2049), (64, 3329), (256, 3329), (128, 3329)])
 def test_fixed_length_lds_k_head_dims(fa, mode, d, n):
