@@ -374,6 +374,26 @@ def test_paged_decode_random_tables(fa, hq, hkv, d):
     assert_close(out, A.paged_decode(q, kc, vc, bt, slt, mnb), what="paged random")
 
 
+@pytest.mark.parametrize("b,sls", [
+    (12, [40, 7, 40, 40, 1, 7, 90, 40, 7, 90, 3, 40]),   # longest first with ties: the order must stay a bijection
+    (600, None),                                          # more sequences than the longest-first limit (natural order)
+])
+def test_paged_decode_ordering(fa, b, sls):
+    """Paged decode serves sequences longest first (ties by index) for up to
+    512 sequences and in index order beyond; every row against the oracle."""
+    g = gen(13)
+    hq, hkv, d, mnb = 4, 2, 64, 6
+    if sls is None:
+        sls = torch.randint(1, 16 * mnb + 1, (b,), generator=g, dtype=torch.int32).tolist()
+    npages = b * mnb
+    bt = torch.randperm(npages, generator=g).int().reshape(b, mnb)
+    kc, vc = randn(g, npages, hkv, 16, d), randn(g, npages, hkv, 16, d)
+    q = randn(g, b, hq, 1, d)
+    slt = torch.tensor(sls, dtype=torch.int32)
+    out = fa.forward_paged_decode_gqa_fp16(*cuda(q, kc, vc, bt, slt), mnb)
+    assert_close(out, A.paged_decode(q, kc, vc, bt, slt, mnb), what=f"paged order b={b}")
+
+
 def test_paged_decode_empty_sequence_is_nan(fa):
     g = gen(5)
     q, kc, vc = randn(g, 2, 4, 1, 64), randn(g, 4, 2, 16, 64), randn(g, 4, 2, 16, 64)
