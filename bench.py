@@ -433,6 +433,21 @@ def measure_ceilings(torch):
         out[f"stream_read_{blocks}wg"] = dict(gbs=nbytes / sec / 1e9, frac_of_peak=nbytes / sec / 1e9 / HBM_PEAK_GBS,
                                               bytes=nbytes, us=sec * 1e6)
     del src
+    # read + write: torch's device copy of 134 MB (config 8's size class), six rotating buffers
+    n = 67 * 1000 * 1000
+    srcs = [torch.empty(n, dtype=torch.uint8, device="cuda").fill_(i) for i in range(6)]
+    dsts = [torch.empty_like(t) for t in srcs]
+    turn = [0]
+
+    def copy():
+        j = turn[0] % 6
+        turn[0] += 1
+        dsts[j].copy_(srcs[j])
+
+    sec = timed(copy, 60)
+    out["copy_read_write_134MB"] = dict(gbs=2 * n / sec / 1e9, frac_of_peak=2 * n / sec / 1e9 / HBM_PEAK_GBS,
+                                        bytes=2 * n, us=sec * 1e6)
+    del srcs, dsts
     iters = 4000
     g = torch.Generator(device="cuda").manual_seed(11)
     for blocks in (256 * 2, 256 * 3):  # 2 or 3 waves per SIMD, each with 4 independent accumulators
