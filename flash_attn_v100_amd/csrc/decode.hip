@@ -84,6 +84,9 @@ constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this 
 #ifndef FA_DEC_PIPE
 #define FA_DEC_PIPE 1
 #endif
+#ifndef FA_DEC_TAIL_FIRST
+#define FA_DEC_TAIL_FIRST 1
+#endif
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
 struct DecodeParams {
@@ -109,7 +112,7 @@ struct DecodeParams {
   int chunk, num_splits, num_hg;
   int max_num_blocks, num_pages;
   int lpt;                     // paged: serve sequences longest first
-  int absorb_tail;             // fixed-length: the last split runs to fixed_len
+  int absorb_tail;             // fixed-length: split 0 also takes the keys past S * chunk
   int seg1, seg_shift;         // contiguous modes: key v < seg1 is row v, later keys row v + seg_shift
                                // (seg_shift = 0: identity; sliding window: sink run, then window run)
   float scale_log2;            // (1/sqrt(D)) * log2(e)
@@ -306,14 +309,26 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
   const int col = (lane % LPR) * 8;
 
   const int L = seq_len_of<MODE>(p, b);
-  const int k0 = split * p.chunk;
-  // With absorb_tail (fixed-length calls only) the last split also takes the
-  // short remainder past (S - 1) * chunk; it stays within kMaxChunk keys.
+  // With absorb_tail (fixed-length calls only) the short remainder past
+  // S * chunk (at most a quarter chunk) goes to split 0: [0, chunk + extra),
+  // then split s takes [extra + s * chunk, +chunk).  Split 0 is dispatched
+  // first, and on a CU shared with a later split's workgroup its waves are the
+  // older ones and win the arbitration: 5b's splits 0-3 finished at 21.8,
+  // 21.7, 24.1 and 26.5 us on average with the remainder on split 3, whose
+  // one-key tile cost its waves a whole extra iteration.
   // Paged: the splits are planned over the table row (16 * max_num_blocks
   // tokens); a longer sequence keeps reading the flat table past its row, as
   // the reference does, and the last split takes all of those keys.
-  const bool last_takes_rest = (p.absorb_tail || MODE == kModePaged) && split == S - 1;
-  const int k1 = last_takes_rest ? L : min(L, k0 + p.chunk);
+  int k0 = split * p.chunk;
+  int k1;
+  if (FA_DEC_TAIL_FIRST && p.absorb_tail) {
+    const int extra = max(0, L - S * p.chunk);
+    k0 = split == 0 ? 0 : extra + split * p.chunk;
+    k1 = min(L, extra + (split + 1) * p.chunk);
+  } else {
+    const bool last_takes_rest = (p.absorb_tail || MODE == kModePaged) && split == S - 1;
+    k1 = last_takes_rest ? L : min(L, k0 + p.chunk);
+  }
 
   if (k0 >= k1) {
     // No key at all (L <= 0): the reference's acc/l_i is 0/0 there.  Split 0
@@ -1093,9 +1108,9 @@ static int pick_dp(int d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
 static int pick_gb(int g) { return g <= 1 ? 1 : (g <= 2 ? 2 : (g <= 4 ? 4 : (g <= 8 ? 8 : 16))); }
 
 // absorb_tail (fixed-length calls): when the keys past the last full chunk
-// are at most a quarter chunk, the last full split takes them too instead of
-// a split of its own (e.g. 4097 keys in 256-key splits: 16 splits, not 17 --
-// one workgroup and one merge round trip less).
+// are at most a quarter chunk, a full split (split 0, in the kernel) takes
+// them too instead of a split of their own (e.g. 4097 keys in 256-key
+// splits: 16 splits, not 17 -- one workgroup and one merge round trip less).
 static DecodePlan make_plan(int B, int H_Q, int H_KV, int max_len, int D, int target_blocks,
                             bool absorb_tail = false, int quantum = kChunkQuantum) {
   DecodePlan pl;
