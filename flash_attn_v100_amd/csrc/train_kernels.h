@@ -348,6 +348,9 @@ struct TileRing {
 #ifndef FA_BWD_REV
 #define FA_BWD_REV 1
 #endif
+#ifndef FA_BWD_GROUP
+#define FA_BWD_GROUP 4
+#endif
 
 struct TrainParams {
   const void* q;
@@ -367,10 +370,19 @@ struct TrainParams {
   float scale_log2;  // scale * log2(e)
 };
 
+// Causal calls deal an XCD's units in groups of kBwdGroupUnits, each group's
+// blocks interleaved heaviest first across its units (the 128-row blocks of
+// a causal unit range from 1 to N/128 tiles of work, so one unit at a time
+// left the lightest blocks of every unit trailing): config 7 350 -> 320 us,
+// 16 x 16 heads x 512 keys 171 -> 148 us; groups of 2 and 8 measured close;
+// non-causal calls (equal blocks) keep one unit at a time.
+constexpr int kBwdGroupUnits = FA_BWD_GROUP;
+__host__ __device__ inline int bwd_group_units(const TrainParams& p) { return p.causal ? kBwdGroupUnits : 1; }
+
 // Workgroup -> ((batch, head) unit bh, 128-row block blk).  With at least 8
 // units, every block of a unit runs on one XCD (the dispatcher deals workgroup
 // j to XCD j % 8), so the unit's streamed tiles are shared through that XCD's
-// L2, and an XCD walks its units one after another, heaviest block first
+// L2, and an XCD walks its units group by group, heaviest block first
 // (heavy_last: the last block carries the most work).  Returns false for the
 // padding workgroups of the last round.
 __device__ __forceinline__ bool map_block(const TrainParams& p, bool heavy_last, int& bh, int& blk) {
@@ -379,8 +391,10 @@ __device__ __forceinline__ bool map_block(const TrainParams& p, bool heavy_last,
   int b;
   if (p.BH >= 8) {
     const int i = j / 8;
-    bh = j % 8 + 8 * (i / nb);
-    b = i % nb;
+    const int gu = bwd_group_units(p);
+    const int group = i / (gu * nb), ii = i % (gu * nb);
+    bh = j % 8 + 8 * (group * gu + ii % gu);
+    b = ii / gu;
     if (bh >= p.BH) return false;
   } else {
     bh = j / nb;
@@ -391,7 +405,8 @@ __device__ __forceinline__ bool map_block(const TrainParams& p, bool heavy_last,
 }
 
 inline int train_grid(const TrainParams& p) {
-  return p.BH >= 8 ? 8 * ceil_div(p.BH, 8) * p.nblk : p.BH * p.nblk;
+  const int gu = bwd_group_units(p);
+  return p.BH >= 8 ? 8 * ceil_div(ceil_div(p.BH, 8), gu) * gu * p.nblk : p.BH * p.nblk;
 }
 
 // Drives a TileRing over `ntiles` tiles starting at row r_first and calls
