@@ -104,6 +104,28 @@ def test_backward_shapes(fa, dtype, causal, b, h, n, d):
     _check_grads((dq, dk, dv), ref, dtype == torch.float16, f"backward {b,h,n,d}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_backward_grouped_units_with_padding(fa, dtype):
+    """Causal calls deal each XCD's (batch, head) units in groups of 4, the
+    blocks of a group heaviest first: 40 units (5 per XCD, so a full group
+    and a group of one unit plus three padding slots) over 3 blocks of 128
+    rows with a partial last block; every gradient against the oracle."""
+    b, h, n, d = 5, 8, 300, 128
+    g = gen(4141)
+    q, k, v, do = (randn(g, b, h, n, d, dtype=dtype) for _ in range(4))
+    qc, kc, vc, dc = cuda(q, k, v, do)
+    fwd = fa.forward_fp16_with_lse if dtype == torch.float16 else fa.forward_with_lse
+    out, lse = fwd(qc, kc, vc, True)
+    dq, dk, dv = fa.backward(dc, qc, kc, vc, out, lse, True)
+    ref = A.backward(do, q, k, v, out.cpu(), lse.cpu(), True)
+    _check_grads((dq, dk, dv), ref, dtype == torch.float16, "grouped units")
+    # the fp32 forward's causal grid is dealt the same way
+    if dtype == torch.float32:
+        ro, rl = A.prefill_lse(q, k, v, True, compute_dtype=F64)
+        assert_close(out, ro, atol=2e-4, rtol=2e-4, what="grouped fp32 forward")
+        assert_close(lse, rl, atol=2e-4, rtol=2e-4, what="grouped fp32 lse")
+
+
 def test_backward_deterministic(fa):
     g = gen(5)
     q, k, v, do = (randn(g, 1, 4, 333, 64) for _ in range(4))
