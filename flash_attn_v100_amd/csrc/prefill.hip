@@ -33,9 +33,10 @@
 // computing at its own diagonal but keeps copying its share of later tiles.
 // Work items are dealt XCD by XCD (the dispatcher sends workgroup j to XCD
 // j % 8): each XCD owns a set of KV heads and runs them in groups of about
-// 128 workgroups (under two resident rounds), heaviest query tile first within a
-// group, so the query tiles that share K/V tiles run together behind one L2
-// and the hardware dispatcher packs the lighter ones into the tail.
+// 128 workgroups (under two resident rounds), heaviest query tile first
+// within a group, so the query tiles that share K/V tiles run together
+// behind one L2 and the hardware dispatcher packs the lighter ones into the
+// tail.
 #include <math.h>
 
 #include <algorithm>
