@@ -90,6 +90,9 @@ constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this 
 #ifndef FA_DEC_PRIO
 #define FA_DEC_PRIO 1
 #endif
+#ifndef FA_DEC_PREFETCH2
+#define FA_DEC_PREFETCH2 1
+#endif
 
 constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
 
@@ -813,6 +816,26 @@ __global__ __launch_bounds__(kDecThreads) void decode_splitkv_kernel(
       }
       return;
     }
+#if FA_DEC_PREFETCH2
+    if constexpr (MODE == kModeDecode && !kLdsK) {
+      // A wave with exactly two iterations (a split that took a short
+      // remainder) issues both tiles' loads before computing either: the
+      // second tile then costs its arithmetic, not another memory round trip
+      // (config 2, where the absorbed remainder gives split 0 two tiles:
+      // 9.3 -> 9.0 us).  Only the small grids that do not stage K in LDS take
+      // this path, so the extra registers cost no occupancy that matters.
+      const int t0 = from + wave * TK;
+      if (t0 + stride < to && t0 + 2 * stride >= to) {
+        Tile A, B;
+        load_tile(A, t0);
+        load_tile(B, t0 + stride);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_tile(A, t0);
+        compute_tile(B, t0 + stride);
+        return;
+      }
+    }
+#endif
     for (int t0 = from + wave * TK; t0 < to; t0 += stride) {
       prio_by_remaining<MODE>((to - t0 + stride - 1) / stride);
       Tile A;
