@@ -76,8 +76,9 @@ constexpr int kFixedQuantum = FA_DEC_FIXED_QUANTUM;  // fixed-length split bound
 // and 26.5 -> 27.1 us).
 constexpr int kTargetBlocksInt8KV = 768;
 constexpr int kInt8KVQuantum = 128;
-constexpr int kMaxSplits = 128;
+constexpr int kMaxSplits = 128;         // splits per sequence, upper bound
 constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this many units run split-major
+// Switches for the measured kernel variants (the same rule: defaults shipped).
 #ifndef FA_DEC_PEEK
 #define FA_DEC_PEEK 1
 #endif
@@ -94,7 +95,7 @@ constexpr int kSplitMajorUnits = 64;  // fixed-length launches of at least this 
 #define FA_DEC_PREFETCH2 1
 #endif
 
-constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences       // splits per sequence, upper bound
+constexpr int kLptMaxSeqs = 512;      // longest-first ordering up to this many sequences
 
 struct DecodeParams {
   const half_t* q;
