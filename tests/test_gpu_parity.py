@@ -794,7 +794,7 @@ def test_sliding_window_reference_case(fa):
 @pytest.mark.parametrize("n", [1025, 1087, 1088, 1089, 2049, 4097, 4160, 4161])
 def test_decode_split_tail_boundaries(fa, n):
     """Fixed-length decode folds a key remainder of at most a quarter chunk into
-    the last split (256-key chunks here: remainders 1, 63, 64 folded; 65 not)."""
+    split 0 (256-key chunks here: remainders 1, 63, 64 folded; 65 not)."""
     g = gen(n)
     q, k, v = randn(g, 1, 32, 1, 128), randn(g, 1, 8, n, 128), randn(g, 1, 8, n, 128)
     out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, n - 1)
@@ -805,6 +805,23 @@ def test_decode_split_tail_boundaries(fa, n):
     o8 = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), n - 1)
     r8 = A.decode_int8(q, k, v, qs, ks, n - 1)
     assert rel_l2(o8, r8) <= INT8_REL_L2
+
+
+@pytest.mark.parametrize("d", [64, 80, 128, 256])
+@pytest.mark.parametrize("n", [129, 257, 300, 513])
+def test_decode_small_grid_two_tile_waves(fa, d, n):
+    """Small contiguous decode grids (no LDS staging) split at 128 keys; a wave
+    with exactly two tiles (every wave at D = 256, whose tiles are 16 keys; the
+    waves of split 0 that take the folded remainder) loads both tiles before
+    computing either.  Against the oracle at several head dims (80: rows not
+    16-byte multiples) and group sizes, and through the sliding-window entry."""
+    for hq, hkv in ((8, 2), (4, 4), (16, 2)):
+        g = gen(7000 + 13 * d + n + hq)
+        q, k, v = randn(g, 1, hq, 1, d), randn(g, 1, hkv, n, d), randn(g, 1, hkv, n, d)
+        out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, n - 1)
+        assert_close(out, A.decode(q, k, v, True, n - 1), what=f"two-tile decode d={d} n={n} {hq}:{hkv}")
+    sw = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, n - 1, n // 2, 4)
+    assert_close(sw, A.decode_sliding_window(q, k, v, n - 1, n // 2, 4), what=f"two-tile window d={d} n={n}")
 
 
 # ---------------------------------------------------------------- many-unit fixed-length launches
