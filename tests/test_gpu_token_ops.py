@@ -174,6 +174,65 @@ def test_speculative_verify_residual_at_a_running_sum(fa):
     assert int(rout[0, 0]) > sums[j][0]  # the first index whose running sum exceeds r
 
 
+def _adversarial_rows(g, shape, kind):
+    """Non-negative float32 rows that stress the exact fp32 running sums: few
+    mantissa bits (round-half-to-even ties and exact binade ends), a dynamic
+    range down to subnormals, mostly zeros, or typical softmax values."""
+    if kind == "ties":
+        m = torch.randint(0, 16, shape, generator=g).float()
+        e = torch.randint(8, 24, shape, generator=g).float()
+        return (m * torch.exp2(-e)).float()
+    if kind == "range":
+        e = torch.randint(0, 140, shape, generator=g).float()
+        return (torch.rand(shape, generator=g) * torch.exp2(-e)).float()
+    if kind == "sparse":
+        x = torch.rand(shape, generator=g) * 1e-3
+        return torch.where(torch.rand(shape, generator=g) < 0.8, torch.zeros(shape), x).float()
+    return torch.softmax(torch.randn(shape, generator=g), -1)
+
+
+@pytest.mark.parametrize("kind", ["ties", "range", "sparse", "softmax"])
+@pytest.mark.parametrize("V", [700, 5000, 32000])
+def test_speculative_verify_exact_sums(fa, kind, V):
+    """Every scan (Z, the residual sample, the sample from the target, the
+    bonus) against the oracle's serial float32 loops on rows built to make the
+    sums' rounding matter, with r set to one of the bonus scan's own running
+    sums (hit exactly at the boundary) on half of the rows."""
+    B, K = 8, 2
+    g = torch.Generator().manual_seed(900 + V + len(kind))
+    tp = _adversarial_rows(g, (B, K + 1, V), kind)
+    dp = _adversarial_rows(g, (B, K, V), kind)
+    dp[1] = tp[1, :K]  # Z == 0 rows: sample from the target itself
+    tok = torch.randint(0, V, (B, K), generator=g)
+    rv = torch.rand(B, K, generator=g)
+    for b in range(0, B, 2):
+        # every step accepted (a token the target gives at least the draft's
+        # mass, r < 1), so the bonus scan of row K runs with r = r_{K-1}, set
+        # to one of that scan's own running sums
+        tok[b] = (tp[b, :K] - dp[b, :K]).argmax(-1)
+        cs = np.cumsum(tp[b, K].numpy().astype(np.float32), dtype=np.float32)
+        j = int(torch.randint(0, V, (1,), generator=g))
+        rv[b] = 0.0
+        if 0 < cs[j] < 1:
+            rv[b, K - 1] = float(cs[j])
+    _check_spec(fa, tp, dp, tok, rv, K)
+
+
+def test_speculative_verify_non_monotone_rows(fa):
+    """Rows with negative and non-finite entries (outside the probability
+    contract) take the plain serial loop and still match the serial oracle."""
+    B, K, V = 4, 2, 3000
+    g = torch.Generator().manual_seed(77)
+    tp = torch.softmax(torch.randn(B, K + 1, V, generator=g), -1)
+    dp = torch.softmax(torch.randn(B, K, V, generator=g), -1)
+    tp[0, K, 100:110] = -1e-3
+    tp[1, :, 2500] = float("inf")
+    tp[2, K, 5] = float("nan")
+    tok = torch.randint(0, V, (B, K), generator=g)
+    rv = torch.rand(B, K, generator=g)
+    _check_spec(fa, tp, dp, tok, rv, K)
+
+
 def test_speculative_verify_validation(fa):
     tp = torch.rand(1, 3, 10, device="cuda")
     dp = torch.rand(1, 2, 10, device="cuda")
