@@ -824,6 +824,32 @@ def test_decode_small_grid_two_tile_waves(fa, d, n):
     assert_close(sw, A.decode_sliding_window(q, k, v, n - 1, n // 2, 4), what=f"two-tile window d={d} n={n}")
 
 
+@pytest.mark.parametrize("mode", ["decode", "window", "int8", "cb"])
+def test_decode_long_context(fa, mode):
+    """One sequence of 300001 keys (8:2 heads): the split length is capped by
+    the 128-split limit rather than the workgroup target, against the oracle."""
+    n, d = 300001, 128
+    g = gen(31000 + len(mode))
+    q, k, v = randn(g, 1, 8, 1, d), randn(g, 1, 2, n, d), randn(g, 1, 2, n, d)
+    if mode == "decode":
+        out = fa.forward_decode_gqa_fp16(*cuda(q, k, v), True, n - 1)
+        assert_close(out, A.decode(q, k, v, True, n - 1), what="long-context decode")
+    elif mode == "window":
+        out = fa.forward_decode_sliding_window_gqa(*cuda(q, k, v), True, n - 1, 70000, 64)
+        assert_close(out, A.decode_sliding_window(q, k, v, n - 1, 70000, 64), what="long-context window")
+    elif mode == "int8":
+        qs = (q.float().abs().amax(-1).squeeze(-1) / 127).contiguous()
+        ks = (k.float().abs().amax((-1, -2)) / 127).unsqueeze(-1).expand(1, 2, n).contiguous()
+        o8 = fa.forward_decode_int8_gqa(*cuda(q, k, v, qs, ks), n - 1)
+        assert rel_l2(o8, A.decode_int8(q, k, v, qs, ks, n - 1)) <= INT8_REL_L2
+    else:
+        # continuous batching: two sequences of the same cache, 300000 and 150000 cached keys
+        q2, k2, v2 = torch.cat([q, q.flip(1)]), torch.cat([k, k.flip(1)]), torch.cat([v, v.flip(1)])
+        cl = torch.tensor([n - 1, 150000], dtype=torch.int32)
+        out = fa.forward_continuous_batching_fp16(*cuda(q2, k2, v2, cl), True)
+        assert_close(out, A.continuous_batching(q2, k2, v2, cl, True), what="long-context continuous batching")
+
+
 # ---------------------------------------------------------------- many-unit fixed-length launches
 
 @pytest.mark.parametrize("mode", ["decode", "window", "int8_cache"])
